@@ -1,0 +1,167 @@
+/*
+ * tilemix_hip.h -- C ABI of the MI355X (gfx950) TileMix prefill library
+ * (libtilemix_hip.so).
+ *
+ * The library replaces the two GPU launches of the reference's prefill hot path:
+ *
+ *   quant_per_block_int8_kernel[grid](...)
+ *       attention/triton/quant_per_block_varlen.py:6-13 (kernel signature)
+ *       attention/triton/quant_per_block_varlen.py:65-73 (launch site)
+ *   attn_fwd[grid](...)
+ *       attention/triton/tilemix.py:503-579 (kernel signature)
+ *       attention/triton/tilemix.py:1286-1336 (launch site in launch_prequantized)
+ *
+ * Conventions (all entry points):
+ *   - Plain C types only: device pointers, element strides, sizes.  No torch
+ *     types cross this boundary.  `stream` is a hipStream_t passed as void*
+ *     (NULL = the default stream).
+ *   - Tensors are token-major "[tokens, heads, dim]" (the reference's flattened
+ *     varlen layout, attention/triton/tilemix.py:1169-1170).  Strides are in
+ *     ELEMENTS; the dim stride must be 1.
+ *   - fp16 data is IEEE binary16 (passed as void*).
+ *   - Every call is asynchronous on `stream`, allocates nothing, never
+ *     synchronises the host and is reentrant.
+ *   - Return value: 0 on success, a TILEMIX_E* code otherwise; the message of
+ *     the last failure on the calling thread is returned by tilemix_last_error().
+ */
+#ifndef TILEMIX_HIP_H
+#define TILEMIX_HIP_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define TILEMIX_ABI_VERSION 1
+
+enum tilemix_status {
+    TILEMIX_OK = 0,
+    TILEMIX_E_INVALID = 1,   /* argument validation failed (nothing launched) */
+    TILEMIX_E_LAUNCH = 2,    /* the HIP runtime rejected the launch */
+};
+
+/* Routing modes, identical codes to the reference
+ * (attention/triton/tilemix.py:159-161: ROUTING_MODE_MIXED/FP16/INT8). */
+enum tilemix_routing_mode {
+    TILEMIX_ROUTING_MIXED = 0,
+    TILEMIX_ROUTING_FP16 = 1,
+    TILEMIX_ROUTING_INT8 = 2,
+};
+
+/*
+ * Per-block symmetric int8 quantisation of a varlen token-major tensor.
+ * Replaces quant_per_block_int8_kernel (attention/triton/quant_per_block_varlen.py:6-45)
+ * and the host arithmetic of per_block_int8_single (:48-75).
+ *
+ * For every sequence b, every block `blk` of `blk_tokens` tokens and every head:
+ *   s    = max|x * sm_scale| / 127           (fp32, IEEE division)
+ *   t    = (x * sm_scale) / s ; t += (t >= 0 ? 0.5 : -0.5)
+ *   code = (int8) trunc(t)                   (code 0 for an all-zero block)
+ * The scale of block blk of sequence b is stored at row cu_seqlens_scale[b] + blk.
+ * cu_seqlens_scale ([batch + 1], int32) is computed and WRITTEN by the launch
+ * (exclusive prefix sum of ceil(L_b / blk_tokens)), so the caller needs no
+ * device->host copy to size it: scale_rows_capacity >= ceil(tokens/blk) + batch
+ * always suffices.
+ */
+typedef struct tilemix_quant_params {
+    const void* input;            /* fp16 [tokens, heads, head_dim]               */
+    int8_t* output;               /* int8 codes, same logical layout               */
+    float* scale;                 /* fp32 [scale_rows_capacity, heads], row-major */
+    void* scale_half;             /* optional fp16 copy of `scale` (NULL = none)  */
+    const int32_t* cu_seqlens;    /* [batch + 1] token offsets                     */
+    int32_t* cu_seqlens_scale;    /* [batch + 1] written by the launch             */
+    int64_t stride_in_token;
+    int64_t stride_in_head;
+    int64_t stride_out_token;
+    int64_t stride_out_head;
+    int64_t scale_rows_capacity;  /* rows allocated in scale / scale_half          */
+    float sm_scale;
+    int32_t heads;
+    int32_t head_dim;             /* multiple of 8, <= 256                         */
+    int32_t blk_tokens;           /* BLK of the reference (BLKQ=128 / BLKK=64)     */
+    int32_t batch;
+    int32_t max_seqlen;
+} tilemix_quant_params;
+
+int tilemix_quant_per_block_int8(const tilemix_quant_params* p, void* stream);
+
+/*
+ * Fused FP16/INT8-routed flash-attention prefill forward.
+ * Replaces attn_fwd (attention/triton/tilemix.py:503-951) launched by
+ * launch_prequantized (:1132-1337).  One launch computes, for every sequence z,
+ * query head h and query block m (block_m rows), the causal/varlen
+ * online-softmax attention over key tiles of block_n = 64 keys, routing each
+ * tile group (block_n_mask keys) to FP16 or INT8 QK^T by bit j of
+ * precision_bitmask[hk * ceil(Lq_z / block_m) + m] (hk = h / (heads_q/heads_k)).
+ *
+ * Supported by this build: block_m in {64, 128}; block_n == 64;
+ * block_n_mask a multiple of 64 with ceil(max_seqlen_k/block_n_mask) <= 64;
+ * head_dim a multiple of 16, <= 128; blkk a multiple of 64; fp16 data.
+ */
+typedef struct tilemix_attn_params {
+    const void* q;                /* fp16 [tokens_q, heads_q, head_dim]            */
+    const void* k;                /* fp16 [tokens_k, heads_k, head_dim]            */
+    const void* v;                /* fp16 [tokens_k, heads_k, head_dim]            */
+    const void* bias;             /* fp16 [*, heads_q, max_q, max_k] or NULL       */
+    void* out;                    /* fp16 [tokens_q, heads_q, head_dim]            */
+    const uint64_t* precision_bitmask; /* [heads_k * ceil(max_seqlen_q/block_m)]   */
+    const int8_t* q8;             /* int8 Q codes (BLKQ blocks)                    */
+    const int8_t* k8;             /* int8 K codes (BLKK blocks)                    */
+    const int8_t* v8;             /* int8 V codes (only if !int8_use_fp16_v)       */
+    const void* sq;               /* fp16 Q scales [rows, heads_q]                 */
+    const void* sk;               /* fp16 K scales [rows, heads_k]                 */
+    const void* sv;               /* fp16 V scales [rows, heads_k] (int8 V only)   */
+    const int32_t* cu_seqlens_q;  /* [batch + 1]                                   */
+    const int32_t* cu_seqlens_k;  /* [batch + 1]                                   */
+    const int32_t* cu_q_scale;    /* [batch + 1]                                   */
+    const int32_t* cu_k_scale;    /* [batch + 1]                                   */
+    const int32_t* cu_v_scale;    /* [batch + 1] (int8 V only)                     */
+    int64_t stride_q_token, stride_q_head;
+    int64_t stride_k_token, stride_k_head;
+    int64_t stride_v_token, stride_v_head;
+    int64_t stride_o_token, stride_o_head;
+    int64_t stride_q8_token, stride_q8_head;
+    int64_t stride_k8_token, stride_k8_head;
+    int64_t stride_v8_token, stride_v8_head;
+    int64_t stride_bias_head, stride_bias_m, stride_bias_n;
+    float sm_scale;               /* softmax scale (default head_dim^-0.5)         */
+    int32_t heads_q, heads_k, head_dim, batch;
+    int32_t max_seqlen_q, max_seqlen_k;
+    int32_t block_m, block_n, block_n_mask;
+    int32_t blkq, blkk;           /* quantisation block sizes of Q and K (and V)  */
+    int32_t causal;
+    int32_t routing_mode;         /* enum tilemix_routing_mode                     */
+    int32_t int8_use_fp16_v;      /* 1: INT8 tiles use fp16 V for PV (hot path)    */
+} tilemix_attn_params;
+
+int tilemix_attn_fwd(const tilemix_attn_params* p, void* stream);
+
+/*
+ * Same computation as tilemix_attn_fwd (same kernel template, a DUMP
+ * instantiation), additionally writing, for every computed (row, key) score:
+ *   qk_i32[(tok_q) * s_tok + h * s_head + key] = exact int32 Q8.K8 accumulator
+ *                                                (INT8-routed tiles only)
+ *   qk_f16[(tok_q) * s_tok + h * s_head + key] = the fp16 score fed to softmax
+ *                                                (before causal masking; both routes)
+ * tok_q is the packed query token index, key is sequence-local.  Entries of
+ * tiles that are not computed (causally skipped, other route) are left as is.
+ * No reference counterpart: this is the observation point for the bit-exact
+ * int32-accumulator parity tests.  Either dump pointer may be NULL.
+ */
+int tilemix_attn_fwd_debug(const tilemix_attn_params* p,
+                           int32_t* qk_i32, void* qk_f16,
+                           int64_t dump_stride_token, int64_t dump_stride_head,
+                           void* stream);
+
+/* Library introspection. */
+int tilemix_abi_version(void);
+/* sizeof() of the parameter structs as compiled into the library: 0 = quant, 1 = attn. */
+int64_t tilemix_params_size(int which);
+const char* tilemix_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* TILEMIX_HIP_H */

@@ -1,0 +1,228 @@
+"""GPU parity of the HIP path against the CPU oracle (same seeded inputs).
+
+Bars: int8 codes / scales / cu_scale and the int32 Q8.K8 accumulators
+bit-exact; the fp16 scores of INT8 tiles bit-exact; attention output within
+max-abs 2e-3 and mean-abs 2e-4 of the fp32 emulation.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import tilemix_oracle as O
+from tests._helpers import (assert_close_out, bitmask_tensor, oracle_quant, packed_inputs, random_bitmask,
+                            to_dev)
+from tilemix_amd.attention import precision_maps as pm
+from tilemix_amd.attention.hip import tilemix as tmx
+from tilemix_amd.attention.hip.quant_per_block_varlen import per_block_int8_single, quantize_blocks
+
+pytestmark = pytest.mark.gpu
+
+
+# ---------------------------------------------------------------- quantisation
+QUANT_CASES = [
+    ("single256", [256], 4, 128),
+    ("ragged", [1, 63, 64, 65, 300], 3, 128),
+    ("with_empty", [1000, 0, 129], 2, 64),
+]
+
+
+@pytest.mark.parametrize("blk", [128, 64])
+@pytest.mark.parametrize("name,lengths,heads,d", QUANT_CASES, ids=[c[0] for c in QUANT_CASES])
+def test_quant_bitexact(device, name, lengths, heads, d, blk):
+    x, _, _, cu = packed_inputs(lengths, heads, 1, d, seed=len(lengths) + blk, outliers=(3, 17))
+    # an all-zero block and a block holding one huge value
+    if lengths[0] >= blk:
+        x[:blk, 0] = 0
+        x[5, 1 % heads, 7] = np.float16(60000.0)
+    codes, scale, scale16, cu_scale = quantize_blocks(to_dev(x, device), to_dev(cu, device), max(lengths), blk,
+                                                      half_scales=True)
+    rc, rs, rcu = O.quant_per_block_int8(x, cu, blk)
+    torch.cuda.synchronize()
+    n = int(rcu[-1])
+    assert cu_scale.cpu().numpy().tolist() == rcu.tolist()
+    got = codes.cpu().numpy()
+    for b in range(len(lengths)):  # tokens outside sequences are not written
+        np.testing.assert_array_equal(got[cu[b]:cu[b + 1]], rc[cu[b]:cu[b + 1]])
+    np.testing.assert_array_equal(scale[:n].cpu().numpy().view(np.uint32), rs.view(np.uint32))
+    np.testing.assert_array_equal(scale16[:n].cpu().numpy().view(np.uint16), rs.astype(np.float16).view(np.uint16))
+
+
+def test_per_block_int8_single_api(device):
+    x, _, _, cu = packed_inputs([300, 77], 2, 1, 64, seed=5)
+    for cu_t in (to_dev(cu, device), torch.from_numpy(cu)):
+        codes, scale, cus = per_block_int8_single(to_dev(x, device), cu_t, 300, BLK=128, sm_scale=1.0)
+        rc, rs, rcu = O.quant_per_block_int8(x, cu, 128)
+        assert cus.dtype == torch.int64 and cus.cpu().tolist() == rcu.tolist()
+        assert tuple(scale.shape) == rs.shape
+        np.testing.assert_array_equal(scale.cpu().numpy(), rs)
+        np.testing.assert_array_equal(codes.cpu().numpy(), rc)
+
+
+def test_quant_sm_scale(device):
+    """sm_scale != 1 multiplies before the max (reference :38-39)."""
+    x, _, _, cu = packed_inputs([200], 2, 1, 64, seed=9)
+    codes, scale, _, _ = quantize_blocks(to_dev(x, device), to_dev(cu, device), 200, 128, sm_scale=0.3)
+    rc, rs, _ = O.quant_per_block_int8(x, cu, 128, sm_scale=0.3)
+    np.testing.assert_array_equal(codes.cpu().numpy(), rc)
+    np.testing.assert_array_equal(scale[:rs.shape[0]].cpu().numpy(), rs)
+
+
+# ------------------------------------------------------------------- attention
+# name, lengths, hq, hk, d, block_m, block_n_mask, causal, mode, int8_use_fp16_v, map
+ATTN_CASES = [
+    ("cfg1_band", [256], 4, 1, 64, 64, 64, True, "mixed", True, "band"),
+    ("mixed_d128_bm128", [512], 6, 2, 128, 128, 64, True, "mixed", True, "rand"),
+    ("fp16_mode", [384], 4, 2, 128, 128, 64, True, "fp16", True, "rand"),
+    ("int8_mode", [384], 4, 2, 128, 128, 64, True, "int8", True, "rand"),
+    ("all_zero_map_mixed", [384], 4, 2, 128, 128, 64, True, "mixed", True, "zero"),
+    ("varlen_ragged", [1, 70, 129, 300, 64], 4, 2, 128, 128, 64, True, "mixed", True, "rand"),
+    ("noncausal", [200, 100], 2, 1, 64, 64, 64, False, "mixed", True, "rand"),
+    ("mask_group2", [600], 4, 1, 128, 128, 128, True, "mixed", True, "rand"),
+    ("int8_v", [300], 4, 2, 128, 128, 64, True, "mixed", False, "rand"),
+    ("hd80", [200], 2, 1, 80, 64, 64, True, "mixed", True, "rand"),
+    ("gqa4_d64_bm128", [700], 8, 2, 64, 128, 64, True, "mixed", True, "rand"),
+]
+
+
+def _bitmask_for(kind, lengths, hk, block_m, block_n_mask, seed):
+    max_len = max(lengths)
+    m_blocks = -(-max_len // block_m)
+    if kind == "rand":
+        return random_bitmask(hk, m_blocks, seed)
+    if kind == "zero":
+        return np.zeros(hk * m_blocks, dtype=np.uint64)
+    if kind == "band":
+        row = pm.make_precision_bitmask(max_len, block_m, block_n_mask, None, percentage=0.5,
+                                        pattern_type="band", pattern_params={}, COMPUTE_BLOCK_N=64)
+        return np.array([int(x) for x in row.tolist()] * hk, dtype=np.uint64)
+    raise ValueError(kind)
+
+
+def _run_case(device, lengths, hq, hk, d, block_m, bnm, causal, mode, int8v, kind, seed):
+    q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=seed, outliers=(1, 9))
+    max_len = max(lengths)
+    bits = _bitmask_for(kind, lengths, hk, block_m, bnm, seed)
+    out, mode_ret = tmx.tilemix_attention_with_quant(
+        to_dev(q, device), to_dev(k, device), to_dev(v, device), to_dev(cu, device), to_dev(cu, device),
+        max_len, max_len, bitmask_tensor(bits, device), block_m=block_m, block_n=64, block_n_mask=bnm,
+        BLKQ=128, BLKK=64, causal=causal, routing_mode=mode, scalar_scales=(block_m == 128),
+        int8_use_fp16_v=int8v)
+    assert mode_ret == mode
+    mode_code = {"mixed": 0, "fp16": 1, "int8": 2}[mode]
+    q8, sq, cuq, k8, sk, cuk = oracle_quant(q, k, cu)
+    extra = {}
+    if not int8v:
+        v8, sv, cuv = O.quant_per_block_int8(v, cu, 64)
+        extra = dict(v8=v8, sv16=sv.astype(np.float16), cu_v_scale=cuv)
+    ref = O.attn_fwd(q, k, v, cu, cu, bits, block_m=block_m, block_n_mask=bnm, causal=causal,
+                     routing_mode=mode_code, q8=q8, k8=k8, sq16=sq.astype(np.float16),
+                     sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk,
+                     int8_use_fp16_v=int8v, **extra)
+    return out.cpu().numpy(), ref, (q, k, v, cu, bits, q8, sq, cuq, k8, sk, cuk)
+
+
+@pytest.mark.parametrize("case", ATTN_CASES, ids=[c[0] for c in ATTN_CASES])
+def test_attention_matches_oracle(device, case):
+    name, lengths, hq, hk, d, block_m, bnm, causal, mode, int8v, kind = case
+    got, ref, _ = _run_case(device, lengths, hq, hk, d, block_m, bnm, causal, mode, int8v, kind, seed=11)
+    assert_close_out(got, ref)
+
+
+@pytest.mark.parametrize("case", [c for c in ATTN_CASES if c[8] != "fp16" and c[9]],
+                         ids=[c[0] for c in ATTN_CASES if c[8] != "fp16" and c[9]])
+def test_int32_accumulators_bitexact(device, case):
+    name, lengths, hq, hk, d, block_m, bnm, causal, mode, int8v, kind = case
+    q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=23, outliers=(1, 9))
+    max_len = max(lengths)
+    bits = _bitmask_for(kind, lengths, hk, block_m, bnm, 23)
+    q8, sq, cuq, k8, sk, cuk = oracle_quant(q, k, cu)
+    mode_code = {"mixed": 0, "fp16": 1, "int8": 2}[mode]
+    out, qk_i32, qk16 = tmx.debug_launch(
+        to_dev(q, device), to_dev(k, device), to_dev(v, device), to_dev(cu, device), to_dev(cu, device),
+        max_len, max_len, bitmask_tensor(bits, device), q8=to_dev(q8, device), k8=to_dev(k8, device),
+        sQ_blocks=to_dev(sq.astype(np.float16), device), sK_blocks=to_dev(sk.astype(np.float16), device),
+        cu_q_scale=to_dev(cuq.astype(np.int32), device), cu_k_scale=to_dev(cuk.astype(np.int32), device),
+        block_m=block_m, block_n_mask=bnm, causal=causal, routing_mode=mode)
+    ref_out, scores = O.attn_fwd(q, k, v, cu, cu, bits, block_m=block_m, block_n_mask=bnm, causal=causal,
+                                 routing_mode=mode_code, q8=q8, k8=k8, sq16=sq.astype(np.float16),
+                                 sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk,
+                                 want_scores=True)
+    gi = qk_i32.cpu().numpy()
+    gf = qk16.cpu().numpy()
+    n_int8 = 0
+    for (z, h), (acc, s16, route) in scores.items():
+        qs, Lq = int(cu[z]), int(cu[z + 1] - cu[z])
+        rows = np.arange(Lq)[:, None]
+        keys = np.arange(Lq)[None, :]
+        valid = (keys <= rows) if causal else np.ones((Lq, Lq), bool)
+        sel = valid & route
+        n_int8 += int(sel.sum())
+        if acc is not None:
+            np.testing.assert_array_equal(gi[qs:qs + Lq, h, :Lq][sel], acc[sel].astype(np.int32))
+        np.testing.assert_array_equal(gf[qs:qs + Lq, h, :Lq][sel].view(np.uint16), s16[sel].view(np.uint16))
+        # fp16-routed scores: the kernel accumulates in fp32 (MFMA), the oracle
+        # exactly; they may differ by one fp16 ulp near a rounding midpoint, or
+        # by a few 2^-12 steps of a small score after cancellation.
+        self_f = valid & ~route
+        if self_f.any():
+            a = gf[qs:qs + Lq, h, :Lq][self_f].astype(np.float32)
+            b = s16[self_f].astype(np.float32)
+            ulp = np.abs(np.spacing(b.astype(np.float16)).astype(np.float32))
+            assert (np.abs(a - b) <= np.maximum(ulp, 2.0 ** -10)).all()
+            assert (a == b).mean() > 0.99
+    assert n_int8 > 0
+    # Given the kernel's own scores, softmax + PV must match the fp32 emulation.
+    dumped = {}
+    for (z, h) in scores:
+        qs, Lq = int(cu[z]), int(cu[z + 1] - cu[z])
+        dumped[(z, h)] = gf[qs:qs + Lq, h, :Lq]
+    ref_given = O.attn_fwd(q, k, v, cu, cu, bits, block_m=block_m, block_n_mask=bnm, causal=causal,
+                           routing_mode=mode_code, q8=q8, k8=k8, sq16=sq.astype(np.float16),
+                           sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk,
+                           qk16_override=lambda z, h: dumped[(z, h)])
+    assert_close_out(out.cpu().numpy(), ref_given)
+
+
+def test_routing_modes_agree_with_maps(device):
+    """mixed with an all-ones (resp. all-zero) map == int8 (resp. fp16) mode, bitwise."""
+    lengths, hq, hk, d = [512], 4, 2, 128
+    q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=3)
+    qd, kd, vd, cud = (to_dev(a, device) for a in (q, k, v, cu))
+    mb = 4
+    ones = bitmask_tensor([(1 << 64) - 1] * (hk * mb), device)
+    zeros = bitmask_tensor([0] * (hk * mb), device)
+    kw = dict(block_m=128, block_n=64, causal=True, int8_use_fp16_v=True)
+    o_mix1, _ = tmx.tilemix_attention_with_quant(qd, kd, vd, cud, cud, 512, 512, ones, routing_mode="mixed", **kw)
+    o_int8, _ = tmx.tilemix_attention_with_quant(qd, kd, vd, cud, cud, 512, 512, ones, routing_mode="int8", **kw)
+    o_mix0, _ = tmx.tilemix_attention_with_quant(qd, kd, vd, cud, cud, 512, 512, zeros, routing_mode="mixed", **kw)
+    o_fp16, _ = tmx.tilemix_attention_with_quant(qd, kd, vd, cud, cud, 512, 512, zeros, routing_mode="fp16", **kw)
+    _, auto = tmx.tilemix_attention_with_quant(qd, kd, vd, cud, cud, 512, 512, ones, routing_mode="auto", **kw)
+    assert auto == "int8"
+    assert torch.equal(o_mix1, o_int8)
+    assert torch.equal(o_mix0, o_fp16)
+
+
+def test_varlen_dense_entry(device):
+    """tilemix_varlen_attention([B,H,T,D]) == packed call; output is the permuted view."""
+    from tilemix_amd.attention.tilemix_varlen import tilemix_varlen_attention
+    B, Hq, Hk, T, D = 2, 4, 2, 256, 64
+    g = torch.Generator().manual_seed(0)
+    q = torch.randn(B, Hq, T, D, generator=g).half().to(device)
+    k = torch.randn(B, Hk, T, D, generator=g).half().to(device)
+    v = torch.randn(B, Hk, T, D, generator=g).half().to(device)
+    row = pm.make_precision_bitmask(T, 64, 64, None, percentage=0.5, pattern_type="sptrans",
+                                    pattern_params={"stride": 64, "c": 16}, COMPUTE_BLOCK_N=64)
+    pmap = row.repeat(Hk).to(device)
+    out = tilemix_varlen_attention(q, k, v, 64, 64, block_n_mask=64, causal=True, scale=D ** -0.5,
+                                   precision_map_all=pmap, candidates=[(64, 64)], flat_lengths=[pmap.numel()])
+    assert out.shape == (B, Hq, T, D)
+    qn = q.permute(0, 2, 1, 3).reshape(B * T, Hq, D).cpu().numpy()
+    kn = k.permute(0, 2, 1, 3).reshape(B * T, Hk, D).cpu().numpy()
+    vn = v.permute(0, 2, 1, 3).reshape(B * T, Hk, D).cpu().numpy()
+    cu = np.arange(0, (B + 1) * T, T)
+    q8, sq, cuq, k8, sk, cuk = oracle_quant(qn, kn, cu)
+    ref = O.attn_fwd(qn, kn, vn, cu, cu, np.array([int(x) for x in pmap.cpu().tolist()], dtype=np.uint64),
+                     block_m=64, block_n_mask=64, causal=True, q8=q8, k8=k8, sq16=sq.astype(np.float16),
+                     sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk)
+    got = out.permute(0, 2, 1, 3).reshape(B * T, Hq, D).cpu().numpy()
+    assert_close_out(got, ref)
