@@ -141,7 +141,9 @@ int tilemix_attn_fwd(const tilemix_attn_params* p, void* stream);
  * Same computation as tilemix_attn_fwd (same kernel template, a DUMP
  * instantiation), additionally writing, for every computed (row, key) score:
  *   qk_i32[(tok_q) * s_tok + h * s_head + key] = exact int32 Q8.K8 accumulator
- *                                                (INT8-routed tiles only)
+ *                                                (INT8-routed tiles), or the bit
+ *                                                pattern of the fp32 MFMA
+ *                                                accumulator (FP16-routed tiles)
  *   qk_f16[(tok_q) * s_tok + h * s_head + key] = the fp16 score fed to softmax
  *                                                (before causal masking; both routes)
  * tok_q is the packed query token index, key is sequence-local.  Entries of
