@@ -1,0 +1,283 @@
+#!/usr/bin/env python3
+"""TileMix prefill attention benchmark on one MI355X (BASELINE.json metric).
+
+Workload: Llama-3.2-3B attention layer, B=8, L=4096,
+24 query / 8 KV heads, head_dim 128, causal, fp16; Q/K ~ N(0,1) with 4 fixed
+outlier channels per head scaled x8, V ~ N(0,1), seeded; SpTrans routing at
+percentage 0.5 (stride 128, c 32).  One step = one call of
+``tilemix_attention_with_quant`` (the reference's cu_seqlens entry): the int8
+quantisation pre-pass plus the fused attention kernel, inputs resident in HBM.
+
+Printed: one JSON line.  ``value`` is effective TOPS of the whole step
+(algorithmic ops 4*B*Hq*D*L(L+1)/2 / step time); ``roofline`` refers to the
+attention kernel alone, timed with HIP events on the launch stream, against
+the blended fp16/int8 MFMA roofline of the routed tile mix; ``cpu_baseline``
+times the CPU oracle (numpy fp32 emulation) on a bounded slice of the same
+workload on this host.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--sweep]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import re
+import statistics
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+if str(REPO) not in sys.path:
+    sys.path.insert(0, str(REPO))
+
+# Published MI355X dense peaks (AMD): fp16 2.5166 PFLOP/s, int8 5.0332 POP/s.
+PEAK_F16 = 2516.6e12
+PEAK_I8 = 5033.2e12
+
+B, HQ, HK, L, D = 8, 24, 8, 4096, 128
+OUTLIER_CHANNELS = (7, 33, 70, 101)
+OUTLIER_SCALE = 8.0
+SEED = 0
+PROFILE_TRAFFIC = REPO / "profiles" / "attn_fwd_cfg2_sptrans50_pmc.txt"
+
+
+def algorithmic_ops(b=B, hq=HQ, d=D, l=L) -> float:
+    """QK^T + PV flops of causal attention including the diagonal."""
+    return 4.0 * b * hq * d * l * (l + 1) / 2.0
+
+
+def int8_fraction(bitmask_row, l=L, block_m=128, block_n_mask=64) -> float:
+    """Fraction of causally executed 64-key tiles routed to INT8."""
+    nt = (l + 63) // 64
+    group = block_n_mask // 64
+    total = routed = 0
+    for m, raw in enumerate(int(x) for x in bitmask_row):
+        n_blocks = min(nt, ((m + 1) * block_m + 63) // 64)
+        for n in range(n_blocks):
+            total += 1
+            routed += (raw >> (n // group)) & 1
+    return routed / total
+
+
+def roofline_seconds(f: float, ops: float) -> float:
+    qk = pv = ops / 2.0
+    return (pv + (1.0 - f) * qk) / PEAK_F16 + f * qk / PEAK_I8
+
+
+def make_inputs(device):
+    import torch
+    g = torch.Generator(device=device)
+    g.manual_seed(SEED)
+    q = torch.randn((B * L, HQ, D), generator=g, device=device, dtype=torch.float32)
+    k = torch.randn((B * L, HK, D), generator=g, device=device, dtype=torch.float32)
+    v = torch.randn((B * L, HK, D), generator=g, device=device, dtype=torch.float32)
+    for c in OUTLIER_CHANNELS:
+        q[:, :, c] *= OUTLIER_SCALE
+        k[:, :, c] *= OUTLIER_SCALE
+    return q.half(), k.half(), v.half()
+
+
+def sptrans_map(p: float, device):
+    from tilemix_amd.attention import precision_maps as pm
+    row = pm.make_precision_bitmask(L, 128, 64, None, percentage=p, pattern_type="sptrans",
+                                    pattern_params={"stride": 128, "c": 32}, COMPUTE_BLOCK_N=64)
+    return row, row.repeat(HK).to(device)
+
+
+def time_steps(fn, steps: int, warmup: int):
+    """Median-free total timing: W untimed steps, then K steps between two syncs."""
+    import torch
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps  # ms per step
+
+
+def time_each(fn, steps: int):
+    """Per-launch HIP-event durations (events on the launch stream)."""
+    import torch
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(steps)]
+    torch.cuda.synchronize()
+    for s, e in ev:
+        s.record()
+        fn()
+        e.record()
+    torch.cuda.synchronize()
+    return [s.elapsed_time(e) for s, e in ev]
+
+
+def read_traffic():
+    """HBM bytes per attention launch from the committed rocprofv3 --pmc summary, if any."""
+    if not PROFILE_TRAFFIC.exists():
+        return None
+    m = re.search(r"traffic_bytes_per_launch:\s*([0-9.eE+]+)", PROFILE_TRAFFIC.read_text())
+    return float(m.group(1)) if m else None
+
+
+def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 1):
+    """Oracle (numpy fp32 emulation) on sequence 0, the first `sample_groups`
+    KV groups (3 query heads each), quantisation included; scaled to TOPS."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+    from oracle import tilemix_oracle as O
+    hq = sample_groups * (HQ // HK)
+    qs = q[:L, :hq].cpu().numpy()
+    ks = k[:L, :sample_groups].cpu().numpy()
+    vs = v[:L, :sample_groups].cpu().numpy()
+    cu = np.array([0, L])
+    bits = np.array([int(x) for x in bitmask_row.tolist()] * sample_groups, dtype=np.uint64)
+    t0 = time.perf_counter()
+    q8, sq, cuq = O.quant_per_block_int8(qs, cu, 128)
+    k8, sk, cuk = O.quant_per_block_int8(ks, cu, 64)
+    O.attn_fwd(qs, ks, vs, cu, cu, bits, block_m=128, block_n_mask=64, causal=True,
+               q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
+               cu_q_scale=cuq, cu_k_scale=cuk)
+    secs = time.perf_counter() - t0
+    ops = algorithmic_ops(b=1, hq=hq)
+    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    return {
+        "value": ops / secs / 1e12,
+        "unit": "TOPS",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": (f"numpy oracle (fp32 emulation incl. int8 quantisation), sequence 0, "
+                   f"{hq} query heads / {sample_groups} KV head of the B8 L4096 SpTrans50 workload; "
+                   f"{secs:.2f} s for {ops:.3e} ops; host {platform.processor() or platform.machine()}, "
+                   f"os.cpu_count()={os.cpu_count()}"),
+        "seconds": secs,
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--sweep", action="store_true", help="also time SpTrans p in {0,.25,.5,.75,1}")
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one MI355X: the TileMix prefill path shards with no exchange "
+              "(by sequence or KV-head group), and multi-GPU runs are not part of this build; "
+              "run with --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    from tilemix_amd.attention.hip import tilemix as tmx
+    from tilemix_amd.attention.hip.tilemix import _quantize_for_launch
+
+    device = torch.device("cuda:0")
+    torch.cuda.set_device(device)
+    q, k, v = make_inputs(device)
+    cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device=device)
+    ops = algorithmic_ops()
+    kw = dict(block_m=128, block_n=64, block_n_mask=64, BLKQ=128, BLKK=64, causal=True,
+              int8_use_fp16_v=True)
+
+    def step_fn(bm, mode="mixed"):
+        return lambda: tmx.tilemix_attention_with_quant(q, k, v, cu, cu, L, L, bm, routing_mode=mode, **kw)
+
+    row50, bm50 = sptrans_map(0.5, device)
+    f50 = int8_fraction(row50.tolist())
+
+    # ---- the metric: whole step (quantisation + attention) ---------------
+    ms = time_steps(step_fn(bm50), args.steps, args.warmup)
+
+    # ---- the dominant kernel alone: prequantised launches ---------------
+    q8, sq, cuq = _quantize_for_launch(q, cu, L, 128)
+    k8, sk, cuk = _quantize_for_launch(k, cu, L, 64)
+    v8, sv, cuv = tmx._dummy_v_quantization_metadata(v, cu)
+
+    def kernel_fn(bm, mode="mixed"):
+        return lambda: tmx.launch_prequantized(
+            q, k, v, cu, cu, L, L, bm, q8=q8, k8=k8, v8=v8, sQ_blocks=sq, sK_blocks=sk, sV_blocks=sv,
+            cu_q_scale=cuq, cu_k_scale=cuk, cu_v_scale=cuv, routing_mode=mode, **kw)
+
+    kernel_fn(bm50)()
+    k_ms = statistics.mean(time_each(kernel_fn(bm50), args.steps))
+    t_roof = roofline_seconds(f50, ops)
+    achieved = ops / (k_ms * 1e-3) / 1e12
+    peak = ops / t_roof / 1e12
+
+    # ---- same kernel, all-FP16 map (mixed mode) and fp16 mode -------------
+    _, bm0 = sptrans_map(0.0, device)
+    k_ms_fp16map = statistics.mean(time_each(kernel_fn(bm0), args.steps))
+    k_ms_fp16mode = statistics.mean(time_each(kernel_fn(bm0, "fp16"), args.steps))
+    ms_fp16map = time_steps(step_fn(bm0), args.steps, 2)
+
+    sweep = None
+    if args.sweep:
+        sweep = {}
+        for p in (0.0, 0.25, 0.5, 0.75, 1.0):
+            row, bmp = sptrans_map(p, device)
+            fp = int8_fraction(row.tolist())
+            kp = statistics.mean(time_each(kernel_fn(bmp), args.steps))
+            sp = time_steps(step_fn(bmp), args.steps, 2)
+            sweep[str(p)] = {"int8_fraction": fp, "step_ms": sp, "kernel_ms": kp,
+                             "kernel_roofline_frac": roofline_seconds(fp, ops) / (kp * 1e-3)}
+
+    cpu = None
+    if not args.no_cpu:
+        cpu = cpu_baseline(q, k, v, row50)
+        cpu.pop("seconds", None)
+
+    traffic = read_traffic()
+    line = {
+        "metric": "attn prefill ms + eff. TOPS (B8xL4096, SpTrans50, 3B shape); e2e prefill ms",
+        "value": ops / (ms * 1e-3) / 1e12,
+        "unit": "TOPS",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": ms,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16+int8",
+        "data": "synthetic (seeded N(0,1) Q/K/V, 4 outlier channels x8 in Q/K)",
+        "config": {
+            "workload": "Llama-3.2-3B attention layer: B=8, L=4096, Hq=24, Hk=8, D=128, causal, "
+                        "SpTrans p=0.5 (stride 128, c 32), block 128x64, tilemix_attention_with_quant",
+            "int8_tile_fraction": f50,
+            "global_batch": B,
+            "seq_len": L,
+        },
+        "roofline": {
+            "bound": "mfma",
+            "achieved": achieved,
+            "peak": peak,
+            "unit": "TFLOP/s",
+            "frac": achieved / peak,
+            "traffic": traffic,
+            "kernel": "attn_fwd_kernel<4,128,mixed>",
+            "kernel_ms": k_ms,
+            "peak_note": "blended: ops / ((PV + (1-f) QK)/2516.6T + f QK/5033.2T), f = INT8 tile fraction",
+        },
+        "cpu_baseline": cpu,
+        "extra": {
+            "step_ms_all_fp16_map": ms_fp16map,
+            "kernel_ms_all_fp16_map": k_ms_fp16map,
+            "kernel_ms_fp16_mode": k_ms_fp16mode,
+            "speedup_vs_all_fp16_map_kernel": k_ms_fp16map / k_ms,
+            "speedup_vs_all_fp16_map_step": ms_fp16map / ms,
+            "quant_plus_launch_ms": ms - k_ms,
+            "sweep": sweep,
+            "e2e_prefill_ms": None,
+        },
+    }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
