@@ -165,6 +165,10 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--sweep", action="store_true", help="also time SpTrans p in {0,.25,.5,.75,1}")
+    ap.add_argument("--kernel-only", type=int, default=0, metavar="N",
+                    help="profiling mode: launch only the SpTrans50 attention kernel N times, print nothing else")
+    ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
+                    help="profiling mode: one device copy of MIB MiB (HBM counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the TileMix prefill path shards with no exchange "
@@ -178,6 +182,14 @@ def main() -> int:
 
     device = torch.device("cuda:0")
     torch.cuda.set_device(device)
+    if args.copy_calibration:
+        n = args.copy_calibration * (1 << 20) // 4
+        src = torch.ones(n, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        print(f"copied {args.copy_calibration} MiB", flush=True)
+        return 0
     q, k, v = make_inputs(device)
     cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device=device)
     ops = algorithmic_ops()
@@ -204,6 +216,12 @@ def main() -> int:
             cu_q_scale=cuq, cu_k_scale=cuk, cu_v_scale=cuv, routing_mode=mode, **kw)
 
     kernel_fn(bm50)()
+    if args.kernel_only:
+        for _ in range(args.kernel_only):
+            kernel_fn(bm50)()
+        torch.cuda.synchronize()
+        print(f"launched attn_fwd_kernel {args.kernel_only + 1} times", flush=True)
+        return 0
     k_ms = statistics.mean(time_each(kernel_fn(bm50), args.steps))
     t_roof = roofline_seconds(f50, ops)
     achieved = ops / (k_ms * 1e-3) / 1e12

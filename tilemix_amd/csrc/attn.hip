@@ -2,6 +2,8 @@
 // and kernel selection (the kernel template is in attn_kernel.h).
 #include "attn_kernel.h"
 
+#include <algorithm>
+
 namespace tmx {
 
 namespace {
@@ -97,6 +99,15 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   }
   if ((dump_i32 || dump_f16) && (p.bias != nullptr || int8v)) {
     set_error("%s: the debug dump supports neither bias nor the int8 V path", fn);
+    return TILEMIX_E_INVALID;
+  }
+
+  // K/V tiles are read through 32-bit raw buffers spanning one sequence.
+  const int64_t span = (int64_t)p.max_seqlen_k *
+                       (int64_t)std::max(std::max(p.stride_k_token, p.stride_v_token) * 2,
+                                         std::max(p.stride_k8_token, p.stride_v8_token));
+  if (span >= ((int64_t)1 << 31)) {
+    set_error("%s: max_seqlen_k * token stride exceeds 2 GiB (%lld bytes)", fn, (long long)span);
     return TILEMIX_E_INVALID;
   }
 

@@ -110,8 +110,15 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
-__device__ __forceinline__ void async_load16(const void* gptr, unsigned char* lds_wave_base) {
-  __builtin_amdgcn_global_load_lds(gptr, (lds_void*)lds_wave_base, 16, 0, 0);
+// Raw buffer over [base, base + bytes): loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// 16 bytes per lane from the buffer straight into LDS: lane l writes
+// lds_wave_base + 16 l (buffer_load_dwordx4 ... lds).
+__device__ __forceinline__ void async_load16(__amdgpu_buffer_rsrc_t rsrc, int voffset, unsigned char* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds_wave_base, 16, voffset, 0, 0, 0);
 }
 
 // Transposed LDS reads (gfx950).  tr16: within each 16-lane group, output lane
@@ -132,7 +139,7 @@ __device__ __forceinline__ i32x2 lds_read_tr8(const unsigned char* p) {
 // MFMA operand reads conflict-free:
 //   K fp16 (row = DP*2 bytes) and K int8 (row = DP bytes): 32 lanes read one
 //     chunk of 32 different rows (ds_read_b128);
-//   V fp16: 16-lane groups read 4 consecutive rows x 32 bytes (ds_read_b64_tr_b16).
+//   V fp16: 32 lanes read 4 consecutive rows x 64 bytes (ds_read_b64_tr_b16).
 template <int ROWB>
 __device__ __forceinline__ int swz_rows(int r) {
   // rows of ROWB bytes; 256/ROWB rows share one 256-byte bank line.
@@ -142,8 +149,8 @@ __device__ __forceinline__ int swz_rows(int r) {
 }
 template <int ROWB>
 __device__ __forceinline__ int swz_v(int r) {
-  if constexpr (ROWB >= 256) return 2 * (r & 3);
-  else return 2 * ((r >> 1) & 1);  // 128-byte rows
+  if constexpr (ROWB >= 256) return 4 * (r & 3);
+  else return 4 * ((r >> 1) & 1);  // 128-byte rows: row pairs share a bank line
 }
 
 template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS>
@@ -247,61 +254,52 @@ attn_fwd_kernel(const AttnKArgs a) {
   };
 
   // ---- asynchronous tile loads (HBM -> LDS, no registers) -----------------
-  // Rows past the sequence end re-read the last valid row: the bytes are
-  // finite and those keys are masked (p = 0), so they contribute exactly 0.
-  const int lastk = max(Lk - 1, 0);
+  // Each tile is fetched through raw buffers based at the tile's first key
+  // and sized to the keys left in the sequence: rows past the end read as 0
+  // (finite bytes for masked keys, which contribute exactly 0 through p = 0).
+  // Per-lane offsets are loop-invariant; the per-tile work is scalar.
+  const int64_t kt_bytes = a.sk_t * 2, vt_bytes = a.sv_t * 2;
+  const int64_t k8t_bytes = a.sk8_t, v8t_bytes = a.sv8_t;
+  const unsigned char* kseq = reinterpret_cast<const unsigned char*>(a.k + (int64_t)k_start * a.sk_t + (int64_t)hk * a.sk_h);
+  const unsigned char* vseq = reinterpret_cast<const unsigned char*>(a.v + (int64_t)k_start * a.sv_t + (int64_t)hk * a.sv_h);
+  const unsigned char* k8seq = MODE != TILEMIX_ROUTING_FP16
+      ? reinterpret_cast<const unsigned char*>(a.k8 + (int64_t)k_start * a.sk8_t + (int64_t)hk * a.sk8_h) : nullptr;
+  const unsigned char* v8seq = INT8V
+      ? reinterpret_cast<const unsigned char*>(a.v8 + (int64_t)k_start * a.sv8_t + (int64_t)hk * a.sv8_h) : nullptr;
+  auto lane_off = [&](int i, int rowb, int64_t tok_bytes, bool vswz) -> int {
+    const int rpi = 1024 / rowb, cpr = rowb / 16;
+    const int r = (i * NW + wave) * rpi + lane / cpr;
+    int sw;
+    if (rowb == 256) sw = vswz ? swz_v<256>(r) : swz_rows<256>(r);
+    else if (rowb == 128) sw = vswz ? swz_v<128>(r) : swz_rows<128>(r);
+    else sw = swz_rows<64>(r);
+    return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
+  };
   auto issue_tile = [&](int n, int route, unsigned char* stage) {
     const int key0 = n * kBN;
+    const int rem = Lk - key0;  // >= 1
     if (route == 0) {
-      constexpr int RPI = 1024 / ROW16;  // rows per 1 KB wave load
-      constexpr int CPR = ROW16 / 16;
+      const auto rs = make_rsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
 #pragma unroll
-      for (int i = 0; i < K16_INS; ++i) {
-        const int blk = i * NW + wave;
-        const int r = blk * RPI + lane / CPR;
-        const int c = (lane % CPR) ^ swz_rows<ROW16>(r);
-        const int key = min(key0 + r, lastk);
-        const f16* src = a.k + (int64_t)(k_start + key) * a.sk_t + (int64_t)hk * a.sk_h + c * 8;
-        async_load16(src, stage + blk * 1024);
-      }
+      for (int i = 0; i < K16_INS; ++i)
+        async_load16(rs, lane_off(i, ROW16, kt_bytes, false), stage + (i * NW + wave) * 1024);
     } else {
-      constexpr int RPI = 1024 / ROW8;
-      constexpr int CPR = ROW8 / 16;
+      const auto rs = make_rsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
 #pragma unroll
-      for (int i = 0; i < K8_INS; ++i) {
-        const int blk = i * NW + wave;
-        const int r = blk * RPI + lane / CPR;
-        const int c = (lane % CPR) ^ swz_rows<ROW8>(r);
-        const int key = min(key0 + r, lastk);
-        const int8_t* src = a.k8 + (int64_t)(k_start + key) * a.sk8_t + (int64_t)hk * a.sk8_h + c * 16;
-        async_load16(src, stage + blk * 1024);
-      }
+      for (int i = 0; i < K8_INS; ++i)
+        async_load16(rs, lane_off(i, ROW8, k8t_bytes, false), stage + (i * NW + wave) * 1024);
     }
     unsigned char* vstage = stage + KBUF;
     if (!INT8V || route == 0) {
-      constexpr int RPI = 1024 / ROW16;
-      constexpr int CPR = ROW16 / 16;
+      const auto rs = make_rsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
 #pragma unroll
-      for (int i = 0; i < V16_INS; ++i) {
-        const int blk = i * NW + wave;
-        const int r = blk * RPI + lane / CPR;
-        const int c = (lane % CPR) ^ swz_v<ROW16>(r);
-        const int key = min(key0 + r, lastk);
-        const f16* src = a.v + (int64_t)(k_start + key) * a.sv_t + (int64_t)hk * a.sv_h + c * 8;
-        async_load16(src, vstage + blk * 1024);
-      }
+      for (int i = 0; i < V16_INS; ++i)
+        async_load16(rs, lane_off(i, ROW16, vt_bytes, true), vstage + (i * NW + wave) * 1024);
     } else {
-      constexpr int RPI = 1024 / ROW8;
-      constexpr int CPR = ROW8 / 16;
+      const auto rs = make_rsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
 #pragma unroll
-      for (int i = 0; i < V8_INS; ++i) {
-        const int blk = i * NW + wave;
-        const int r = blk * RPI + lane / CPR;
-        const int c = (lane % CPR) ^ swz_rows<ROW8>(r);
-        const int key = min(key0 + r, lastk);
-        const int8_t* src = a.v8 + (int64_t)(k_start + key) * a.sv8_t + (int64_t)hk * a.sv8_h + c * 16;
-        async_load16(src, vstage + blk * 1024);
-      }
+      for (int i = 0; i < V8_INS; ++i)
+        async_load16(rs, lane_off(i, ROW8, v8t_bytes, false), vstage + (i * NW + wave) * 1024);
     }
   };
 
