@@ -8,9 +8,10 @@
 // plus the host-side scale bookkeeping of per_block_int8_single (:55-63),
 // done on the device so no device->host copy is needed to size the output.
 //
-// One workgroup owns one (block, head, sequence); the block is HBM-streamed
-// twice (max pass, code pass -- the second read hits L2: a 128x128 fp16 block
-// is 32 KB).
+// One workgroup owns one (block, head, sequence).  Blocks of up to
+// kRegChunks * 256 eight-element chunks (BLK * D <= 16384: every Q/K block of
+// the hot path) are read from HBM once and held in registers between the max
+// pass and the code pass; larger blocks are streamed twice.
 #include "common.h"
 
 namespace tmx {
@@ -18,6 +19,7 @@ namespace tmx {
 namespace {
 
 constexpr int kQuantThreads = 256;
+constexpr int kRegChunks = 8;
 
 struct QuantKArgs {
   const f16* in;
@@ -78,28 +80,12 @@ __global__ void __launch_bounds__(kQuantThreads) quant_per_block_int8_kernel(con
   const f16* in = a.in + tok0 * a.si_t + (int64_t)h * a.si_h;
   int8_t* out = a.out + tok0 * a.so_t + (int64_t)h * a.so_h;
 
-  float amax = 0.0f;
-  for (int c = tid; c < chunks; c += kQuantThreads) {
-    const int r = c / cpr, col = (c - r * cpr) << 3;
-    const f16x8 x = *reinterpret_cast<const f16x8*>(in + (int64_t)r * a.si_t + col);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)x[e] * a.sm_scale));
-  }
-  amax = wave_max(amax);
-  if (lane == 0) red_f[wave] = amax;
-  __syncthreads();
-  amax = red_f[0];
-#pragma unroll
-  for (int w = 1; w < kQuantThreads / 64; ++w) amax = fmaxf(amax, red_f[w]);
-
-  const float s = amax / 127.0f;  // IEEE division (no fast-math in this build)
-  for (int c = tid; c < chunks; c += kQuantThreads) {
-    const int r = c / cpr, col = (c - r * cpr) << 3;
-    const f16x8 x = *reinterpret_cast<const f16x8*>(in + (int64_t)r * a.si_t + col);
+  const float sm = a.sm_scale;
+  auto encode = [&](const f16x8& x, float s, int r, int col) {
     uint32_t w0 = 0, w1 = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float t = ((float)x[e] * a.sm_scale) / s;
+      float t = ((float)x[e] * sm) / s;
       t += (t >= 0.0f) ? 0.5f : -0.5f;
       // An all-zero block gives 0/0; its codes are defined as 0.
       const int code = (s == 0.0f) ? 0 : (int)t;
@@ -108,6 +94,53 @@ __global__ void __launch_bounds__(kQuantThreads) quant_per_block_int8_kernel(con
       else w1 |= byte << (8 * (e - 4));
     }
     *reinterpret_cast<uint2*>(out + (int64_t)r * a.so_t + col) = make_uint2(w0, w1);
+  };
+  auto block_max = [&](float amax) {
+    amax = wave_max(amax);
+    if (lane == 0) red_f[wave] = amax;
+    __syncthreads();
+    amax = red_f[0];
+#pragma unroll
+    for (int w = 1; w < kQuantThreads / 64; ++w) amax = fmaxf(amax, red_f[w]);
+    return amax;
+  };
+
+  float s;
+  if (chunks <= kRegChunks * kQuantThreads) {
+    f16x8 xs[kRegChunks];
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRegChunks; ++i) {
+      const int c = tid + i * kQuantThreads;
+      if (c < chunks) {
+        const int r = c / cpr, col = (c - r * cpr) << 3;
+        xs[i] = *reinterpret_cast<const f16x8*>(in + (int64_t)r * a.si_t + col);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)xs[i][e] * sm));
+      }
+    }
+    s = block_max(amax) / 127.0f;  // IEEE division (no fast-math in this build)
+#pragma unroll
+    for (int i = 0; i < kRegChunks; ++i) {
+      const int c = tid + i * kQuantThreads;
+      if (c < chunks) {
+        const int r = c / cpr, col = (c - r * cpr) << 3;
+        encode(xs[i], s, r, col);
+      }
+    }
+  } else {
+    float amax = 0.0f;
+    for (int c = tid; c < chunks; c += kQuantThreads) {
+      const int r = c / cpr, col = (c - r * cpr) << 3;
+      const f16x8 x = *reinterpret_cast<const f16x8*>(in + (int64_t)r * a.si_t + col);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)x[e] * sm));
+    }
+    s = block_max(amax) / 127.0f;
+    for (int c = tid; c < chunks; c += kQuantThreads) {
+      const int r = c / cpr, col = (c - r * cpr) << 3;
+      encode(*reinterpret_cast<const f16x8*>(in + (int64_t)r * a.si_t + col), s, r, col);
+    }
   }
   if (tid == 0) {
     const int64_t row = (int64_t)base + blk;
