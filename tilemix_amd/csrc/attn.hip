@@ -1,6 +1,6 @@
 // Host side of tilemix_attn_fwd / tilemix_attn_fwd_debug: argument validation
-// and kernel selection (the kernel template is in attn_kernel.h).
-#include "attn_kernel.h"
+// and kernel selection (kernels: attn_kernel32.h, attn_kernel16.h; selection in attn_launch.h).
+#include "attn_common.h"
 
 #include <algorithm>
 
@@ -168,13 +168,12 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.blkq = p.blkq > 0 ? p.blkq : 1;
   a.blkk = p.blkk > 0 ? p.blkk : kBN;
   a.causal = p.causal ? 1 : 0;
+  const bool dump = dump_i32 != nullptr || dump_f16 != nullptr;
   a.total_items = (int)total;
   a.per_xcd = (int)((total + 7) / 8);
 
-  const int nw = p.block_m / 32;
   const int dp = p.head_dim <= 64 ? 64 : 128;
-  dispatch_attn(a, nw, dp, p.routing_mode, int8v, dump_i32 != nullptr || dump_f16 != nullptr,
-                p.bias != nullptr, stream);
+  dispatch_attn(a, p.block_m, dp, p.routing_mode, int8v, dump, p.bias != nullptr, stream);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     set_error("%s: launch failed: %s", fn, hipGetErrorString(err));
@@ -187,15 +186,15 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
 
 namespace tmx {
 
-void dispatch_attn_main(const AttnKArgs& a, int nw, int dp, int mode, bool int8v, hipStream_t stream);
-void dispatch_attn_bias(const AttnKArgs& a, int nw, int dp, int mode, bool int8v, hipStream_t stream);
-void dispatch_attn_dump(const AttnKArgs& a, int nw, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_main(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_bias(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_dump(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, hipStream_t stream);
 
-void dispatch_attn(const AttnKArgs& a, int nw, int dp, int mode, bool int8v, bool dump, bool bias,
+void dispatch_attn(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, bool dump, bool bias,
                    hipStream_t stream) {
-  if (dump) dispatch_attn_dump(a, nw, dp, mode, int8v, stream);
-  else if (bias) dispatch_attn_bias(a, nw, dp, mode, int8v, stream);
-  else dispatch_attn_main(a, nw, dp, mode, int8v, stream);
+  if (dump) dispatch_attn_dump(a, block_m, dp, mode, int8v, stream);
+  else if (bias) dispatch_attn_bias(a, block_m, dp, mode, int8v, stream);
+  else dispatch_attn_main(a, block_m, dp, mode, int8v, stream);
 }
 
 }  // namespace tmx

@@ -1,0 +1,159 @@
+// Shared pieces of the attention kernels: argument block, numerics helpers,
+// LDS access primitives and swizzles.
+#pragma once
+
+#include "common.h"
+
+#include <math.h>
+
+namespace tmx {
+
+constexpr int kBN = 64;  // keys per compute tile (block_n)
+
+struct AttnKArgs {
+  const f16* q;
+  const f16* k;
+  const f16* v;
+  const f16* bias;
+  f16* out;
+  const uint64_t* bitmask;
+  const int8_t* q8;
+  const int8_t* k8;
+  const int8_t* v8;
+  const f16* sq;
+  const f16* sk;
+  const f16* sv;
+  const int32_t* cu_q;
+  const int32_t* cu_k;
+  const int32_t* cu_qs;
+  const int32_t* cu_ks;
+  const int32_t* cu_vs;
+  int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, so_t, so_h;
+  int64_t sq8_t, sq8_h, sk8_t, sk8_h, sv8_t, sv8_h;
+  int64_t sb_h, sb_m, sb_n;
+  int32_t* dump_i32;
+  f16* dump_f16;
+  int64_t dump_t, dump_h;
+  float qk_scale;
+  int hq, hk, group, d;
+  int m_blocks;   // ceil(max_seqlen_q / block_m)
+  int mask_tiles; // block_n_mask / block_n
+  int blkq, blkk;
+  int causal;
+  int total_items;  // (sequence, query head, query block) work items
+  int per_xcd;
+};
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// fp32(h) - m with one rounding (v_fma_mix: the fp16 operand is converted exactly).
+__device__ __forceinline__ float sub_lo(uint32_t h2, float negm) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(negm));
+  return r;
+}
+__device__ __forceinline__ float sub_hi(uint32_t h2, float negm) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(negm));
+  return r;
+}
+
+// Packed fp16 max without the operand canonicalisation the generic builtin
+// adds (the operands are conversion results or -inf: never signalling NaNs).
+__device__ __forceinline__ uint32_t pk_max(uint32_t x, uint32_t y) {
+  uint32_t r;
+  asm("v_pk_max_f16 %0, %1, %2" : "=v"(r) : "v"(x), "v"(y));
+  return r;
+}
+
+// Materialise an fp32 value.  The reference rounds to fp32 and then to fp16
+// (Triton: mul.f32 / fma, then cvt.rn.f16.f32); without this barrier the
+// compiler fuses fptrunc(fma(a, b, c)) / fptrunc(fmul(a, b)) into one
+// v_fma_mix*_f16, a single rounding that differs on double ties.
+__device__ __forceinline__ float fp32_round(float x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
+  f16x2 v;
+  v[0] = (f16)a;
+  v[1] = (f16)b;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Lane pairs (l, l^16) and (l, l^32): returns {value of the lower lane, value
+// of the upper lane} on both lanes, so op(x, y) is bitwise identical on both.
+__device__ __forceinline__ float2 pair16(float x) {
+  auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float2 pair32(float x) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+// Raw buffer over [base, base + bytes): loads at offsets >= bytes return 0.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+// 16 bytes per lane from the buffer straight into LDS: lane l writes
+// lds_wave_base + 16 l (buffer_load_dwordx4 ... lds).
+__device__ __forceinline__ void async_load16(__amdgpu_buffer_rsrc_t rsrc, int voffset, unsigned char* lds_wave_base) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds_wave_base, 16, voffset, 0, 0, 0);
+}
+
+// Transposed LDS reads (gfx950).  tr16: within each 16-lane group, output lane
+// i, element c = element (i % 4) of the 8 bytes addressed by lane 4c + i/4.
+// tr8: output lane i, byte b = byte (i % 8) of the 8 bytes addressed by lane
+// 2b + i/8.
+__device__ __forceinline__ f16x4 lds_read_tr16(const unsigned char* p) {
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
+  return __builtin_bit_cast(f16x4, v);
+}
+__device__ __forceinline__ i32x2 lds_read_tr8(const unsigned char* p) {
+  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)p);
+}
+
+// ---- LDS layouts ----------------------------------------------------------
+// All tiles are 64 rows (keys).  A row is split in 16-byte chunks; logical
+// chunk c of row r lives at physical chunk c ^ swz(r).  Each swizzle spreads
+// one LDS pass (16 lanes of ds_read_b128, 32 lanes of a transposed b64 read)
+// over all 64 banks:
+//   K fp16 / int8 (ds_read_b128): 16 lanes read one chunk of 16 consecutive rows;
+//   V fp16 (ds_read_b64_tr_b16): 32 lanes read 2 chunks of 8 consecutive rows;
+//   V int8 (ds_read_b64_tr_b8): 32 lanes read 1 chunk of rows {0..7, 16..23} + 32 ks.
+template <int ROWB>
+__device__ __forceinline__ int swz_k(int r) {
+  if constexpr (ROWB >= 256) return r & 15;
+  else if constexpr (ROWB == 128) return (r >> 1) & 7;
+  else return (r >> 2) & 3;  // 64-byte rows
+}
+template <int ROWB>
+__device__ __forceinline__ int swz_v(int r) {
+  if constexpr (ROWB >= 256) return 2 * (r & 7);
+  else return 2 * ((r >> 1) & 3);  // 128-byte rows
+}
+// The 32-row kernel reads V with 16 lanes x 4 rows x 64 bytes per pass
+// (ds_read_b64_tr_b16 over a 32-wide d block).
+template <int ROWB>
+__device__ __forceinline__ int swz_v32(int r) {
+  if constexpr (ROWB >= 256) return 4 * (r & 3);
+  else return 4 * ((r >> 1) & 1);  // 128-byte rows: row pairs share a bank line
+}
+template <int ROWB>
+__device__ __forceinline__ int swz_v8(int r) {
+  if constexpr (ROWB >= 128) return ((r >> 1) & 3) | ((r >> 2) & 4);
+  else return (r >> 2) & 3;  // 64-byte rows
+}
+
+// Launch one instantiation (defined in attn_inst_*.hip).
+void dispatch_attn(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, bool dump, bool bias,
+                   hipStream_t stream);
+
+}  // namespace tmx

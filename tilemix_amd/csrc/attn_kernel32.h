@@ -1,4 +1,5 @@
-// Fused FP16/INT8-routed flash-attention prefill forward for gfx950 (kernel template).
+// Fused FP16/INT8-routed flash-attention prefill forward for gfx950: the
+// 32-row kernel (block_m = 128: 4 waves x 32 query rows).
 //
 // Numerics follow attn_fwd (attention/triton/tilemix.py:503-951):
 //   qk_scale = fp32(sm_scale) * fp32(log2 e)                               (:641)
@@ -32,130 +33,15 @@
 //     share K/V (GQA) and all query blocks of a head hit the same L2; within a
 //     group, query blocks are issued longest-first (causal).
 #pragma once
+#pragma once
 
-#include "common.h"
-
-#include <math.h>
+#include "attn_common.h"
 
 namespace tmx {
 
-constexpr int kBN = 64;  // keys per compute tile (block_n)
-
-struct AttnKArgs {
-  const f16* q;
-  const f16* k;
-  const f16* v;
-  const f16* bias;
-  f16* out;
-  const uint64_t* bitmask;
-  const int8_t* q8;
-  const int8_t* k8;
-  const int8_t* v8;
-  const f16* sq;
-  const f16* sk;
-  const f16* sv;
-  const int32_t* cu_q;
-  const int32_t* cu_k;
-  const int32_t* cu_qs;
-  const int32_t* cu_ks;
-  const int32_t* cu_vs;
-  int64_t sq_t, sq_h, sk_t, sk_h, sv_t, sv_h, so_t, so_h;
-  int64_t sq8_t, sq8_h, sk8_t, sk8_h, sv8_t, sv8_h;
-  int64_t sb_h, sb_m, sb_n;
-  int32_t* dump_i32;
-  f16* dump_f16;
-  int64_t dump_t, dump_h;
-  float qk_scale;
-  int hq, hk, group, d;
-  int m_blocks;   // ceil(max_seqlen_q / block_m)
-  int mask_tiles; // block_n_mask / block_n
-  int blkq, blkk;
-  int causal;
-  int total_items;
-  int per_xcd;
-};
-
-typedef __attribute__((address_space(3))) void lds_void;
-typedef __attribute__((address_space(3))) unsigned char lds_u8;
-typedef short s16x4 __attribute__((ext_vector_type(4)));
-typedef int i32x2 __attribute__((ext_vector_type(2)));
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// fp32(h) - m with one rounding (v_fma_mix: the fp16 operand is converted exactly).
-__device__ __forceinline__ float sub_lo(uint32_t h2, float negm) {
-  float r;
-  asm volatile("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(negm));
-  return r;
-}
-__device__ __forceinline__ float sub_hi(uint32_t h2, float negm) {
-  float r;
-  asm volatile("v_fma_mix_f32 %0, %1, 1.0, %2 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(negm));
-  return r;
-}
-
-// Materialise an fp32 value.  The reference rounds to fp32 and then to fp16
-// (Triton: mul.f32 / fma, then cvt.rn.f16.f32); without this barrier the
-// compiler fuses fptrunc(fma(a, b, c)) / fptrunc(fmul(a, b)) into one
-// v_fma_mix*_f16, a single rounding that differs on double ties.
-__device__ __forceinline__ float fp32_round(float x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
-__device__ __forceinline__ uint32_t pack_h2(float a, float b) {
-  f16x2 v;
-  v[0] = (f16)a;
-  v[1] = (f16)b;
-  return __builtin_bit_cast(uint32_t, v);
-}
-
-// Raw buffer over [base, base + bytes): loads at offsets >= bytes return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
-
-// 16 bytes per lane from the buffer straight into LDS: lane l writes
-// lds_wave_base + 16 l (buffer_load_dwordx4 ... lds).
-__device__ __forceinline__ void async_load16(__amdgpu_buffer_rsrc_t rsrc, int voffset, unsigned char* lds_wave_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds_wave_base, 16, voffset, 0, 0, 0);
-}
-
-// Transposed LDS reads (gfx950).  tr16: within each 16-lane group, output lane
-// i, element c = element (i % 4) of the 8 bytes addressed by lane 4c + i/4.
-// tr8: output lane i, byte b = byte (i % 8) of the 8 bytes addressed by lane
-// 2b + i/8.
-__device__ __forceinline__ f16x4 lds_read_tr16(const unsigned char* p) {
-  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
-  return __builtin_bit_cast(f16x4, v);
-}
-__device__ __forceinline__ i32x2 lds_read_tr8(const unsigned char* p) {
-  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)p);
-}
-
-// ---- LDS layouts ----------------------------------------------------------
-// All tiles are 64 rows (keys).  A row is split in 16-byte chunks; logical
-// chunk c of row r lives at physical chunk c ^ swz(r).  The swizzles make the
-// MFMA operand reads conflict-free:
-//   K fp16 (row = DP*2 bytes) and K int8 (row = DP bytes): 32 lanes read one
-//     chunk of 32 different rows (ds_read_b128);
-//   V fp16: 32 lanes read 4 consecutive rows x 64 bytes (ds_read_b64_tr_b16).
-template <int ROWB>
-__device__ __forceinline__ int swz_rows(int r) {
-  // rows of ROWB bytes; 256/ROWB rows share one 256-byte bank line.
-  if constexpr (ROWB >= 256) return r & 15;
-  else if constexpr (ROWB == 128) return (r >> 1) & 7;
-  else return (r >> 2) & 3;  // 64-byte rows
-}
-template <int ROWB>
-__device__ __forceinline__ int swz_v(int r) {
-  if constexpr (ROWB >= 256) return 4 * (r & 3);
-  else return 4 * ((r >> 1) & 1);  // 128-byte rows: row pairs share a bank line
-}
-
 template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
-attn_fwd_kernel(const AttnKArgs a) {
+attn32_kernel(const AttnKArgs a) {
   constexpr int BM = NW * 32;
   constexpr int KS16 = DP / 16;  // fp16 MFMA k-steps (32x32x16)
   constexpr int KS8 = DP / 32;   // int8 MFMA k-steps (32x32x32)
@@ -175,7 +61,7 @@ attn_fwd_kernel(const AttnKArgs a) {
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l32 = lane & 31;
   const int hi = lane >> 5;
 
@@ -270,9 +156,9 @@ attn_fwd_kernel(const AttnKArgs a) {
     const int rpi = 1024 / rowb, cpr = rowb / 16;
     const int r = (i * NW + wave) * rpi + lane / cpr;
     int sw;
-    if (rowb == 256) sw = vswz ? swz_v<256>(r) : swz_rows<256>(r);
-    else if (rowb == 128) sw = vswz ? swz_v<128>(r) : swz_rows<128>(r);
-    else sw = swz_rows<64>(r);
+    if (rowb == 256) sw = vswz ? swz_v32<256>(r) : swz_k<256>(r);
+    else if (rowb == 128) sw = vswz ? swz_v32<128>(r) : swz_k<128>(r);
+    else sw = swz_k<64>(r);
     return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
   };
   auto issue_tile = [&](int n, int route, unsigned char* stage) {
@@ -304,12 +190,20 @@ attn_fwd_kernel(const AttnKArgs a) {
   };
 
   // ---- online softmax state (one query row per lane) ----------------------
+  // l_i is this lane's share of the row sum; both lanes of a row start at
+  // 1.0 like the reference's l: the first tile with a valid key has
+  // alpha = 0, and a row with no valid key keeps acc = 0, so the start value
+  // never reaches the output.
   float m_i = -INFINITY;
   float l_i = 1.0f;
   f32x16 acc[NDB];
 #pragma unroll
   for (int db = 0; db < NDB; ++db) acc[db] = (f32x16){};
 
+  // The magic bias as an MFMA C operand (first k-step of every INT8 tile).
+  const i32x16 kMagicC = {0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000,
+                         0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000,
+                         0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
   int route_next = 0;
   if (n_blocks > 0) {
     route_next = route_of(0);
@@ -343,7 +237,7 @@ attn_fwd_kernel(const AttnKArgs a) {
         const int r = kb * 32 + l32;
 #pragma unroll
         for (int ks = 0; ks < KS16; ++ks) {
-          const int ch = (2 * ks + hi) ^ swz_rows<ROW16>(r);
+          const int ch = (2 * ks + hi) ^ swz_k<ROW16>(r);
           const f16x8 av = *reinterpret_cast<const f16x8*>(stage + r * ROW16 + ch * 16);
           c = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[ks], c, 0, 0, 0);
         }
@@ -380,14 +274,12 @@ attn_fwd_kernel(const AttnKArgs a) {
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         i32x16 c;
-#pragma unroll
-        for (int rr = 0; rr < 16; ++rr) c[rr] = 0x4B400000;
         const int r = kb * 32 + l32;
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) {
-          const int ch = (2 * ks + hi) ^ swz_rows<ROW8>(r);
+          const int ch = (2 * ks + hi) ^ swz_k<ROW8>(r);
           const i32x4 av = *reinterpret_cast<const i32x4*>(stage + r * ROW8 + ch * 16);
-          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], ks == 0 ? kMagicC : c, 0, 0, 0);
         }
         if (DUMP && a.dump_i32 != nullptr && row_ok) {
 #pragma unroll
@@ -445,12 +337,11 @@ attn_fwd_kernel(const AttnKArgs a) {
     }
 
     // ---- online softmax (reference _softmax_prefix_update) -------------
-    f16x2 mx2 = __builtin_bit_cast(f16x2, s16[0][0]);
+    uint32_t t8[8];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int j = (kb == 0 ? 1 : 0); j < 8; ++j)
-        mx2 = __builtin_elementwise_max(mx2, __builtin_bit_cast(f16x2, s16[kb][j]));
+    for (int j = 0; j < 8; ++j) t8[j] = pk_max(s16[0][j], s16[1][j]);
+    const f16x2 mx2 = __builtin_bit_cast(
+        f16x2, pk_max(pk_max(pk_max(t8[0], t8[1]), pk_max(t8[2], t8[3])), pk_max(pk_max(t8[4], t8[5]), pk_max(t8[6], t8[7]))));
     float mx = fmaxf((float)mx2[0], (float)mx2[1]);
     {
       const float2 sw = swap_halves(mx);
@@ -459,30 +350,24 @@ attn_fwd_kernel(const AttnKArgs a) {
     const bool has = mx != -INFINITY;
     const float m_next = has ? fmaxf(m_i, mx) : m_i;
     const float alpha = has ? fast_exp2(m_i - m_next) : 1.0f;
-    const float negm = -m_next;
-    uint32_t p16[2][8];
+    // With no valid key yet the tile is all -inf and p must be 0: subtract 0.
+    const float negm = m_next == -INFINITY ? 0.0f : -m_next;
+    // P^T as the B operands of the PV MFMAs: pv[ks] holds keys 16 ks .. 16 ks + 15
+    // of this lane's slots (pairs (kb, j) with ks = 2 kb + j / 4).
+    u32x4 pv[4];
     float ls = 0.0f;
-    if (has) {
-      const f16x2 ones = {(f16)1.0f, (f16)1.0f};
+    const f16x2 ones = {(f16)1.0f, (f16)1.0f};
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const float e0 = fast_exp2(sub_lo(s16[kb][j], negm));
-          const float e1 = fast_exp2(sub_hi(s16[kb][j], negm));
-          p16[kb][j] = pack_h2(e0, e1);
-          ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p16[kb][j]), ones, ls, false);
-        }
-    } else {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j) p16[kb][j] = 0u;
-    }
-    {
-      const float2 sw = swap_halves(ls);
-      ls = sw.x + sw.y;
-    }
+      for (int j = 0; j < 8; ++j) {
+        const float e0 = fast_exp2(sub_lo(s16[kb][j], negm));
+        const float e1 = fast_exp2(sub_hi(s16[kb][j], negm));
+        const uint32_t pp = pack_h2(e0, e1);
+        pv[2 * kb + (j >> 2)][j & 3] = pp;
+        ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, pp), ones, ls, false);
+      }
+    // Per-lane share of the row sum (the row's two lanes are combined at the end).
     l_i = l_i * alpha + ls;
     m_i = m_next;
     // alpha == 1 makes the reference's rescale an exact no-op: skip it when
@@ -503,12 +388,9 @@ attn_fwd_kernel(const AttnKArgs a) {
         const int idx = min(vb + key0 / a.blkk, ve - 1);
         sv16 = a.sv[(int64_t)idx * a.hk + hk];
       }
-      const f16x2 sv2 = {sv16, sv16};
+      const f16x8 sv8 = {sv16, sv16, sv16, sv16, sv16, sv16, sv16, sv16};
 #pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int j = 0; j < 8; ++j)
-          p16[kb][j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, p16[kb][j]) * sv2);
+      for (int ks = 0; ks < 4; ++ks) pv[ks] = __builtin_bit_cast(u32x4, __builtin_bit_cast(f16x8, pv[ks]) * sv8);
     }
 
     // ---- O^T += V^T . P^T ----------------------------------------------
@@ -527,7 +409,7 @@ attn_fwd_kernel(const AttnKArgs a) {
           for (int h2 = 0; h2 < 2; ++h2) {
             const int vr = 16 * ks + 8 * h2 + 4 * hi + (j16 >> 2);
             const int col = 32 * db + 16 * g16 + 4 * (j16 & 3);
-            const int ch = (col >> 3) ^ swz_v<ROW16>(vr);
+            const int ch = (col >> 3) ^ swz_v32<ROW16>(vr);
             const unsigned char* p = vst + vr * ROW16 + ch * 16 + (col & 7) * 2;
             const f16x4 v4 = lds_read_tr16(p);
             av[4 * h2 + 0] = v4[0];
@@ -541,27 +423,23 @@ attn_fwd_kernel(const AttnKArgs a) {
           const int jj = j16 >> 1;  // key slot t of this input lane
           const int vr = 16 * ks + 8 * (jj >> 2) + 4 * hi + (jj & 3);
           const int col = 32 * db + 16 * g16 + 8 * (j16 & 1);
-          const int ch = (col >> 4) ^ swz_rows<ROW8>(vr);
+          const int ch = (col >> 4) ^ swz_k<ROW8>(vr);
           const unsigned char* p = vst + vr * ROW8 + ch * 16 + (col & 15);
           const i32x2 w = lds_read_tr8(p);
 #pragma unroll
           for (int e = 0; e < 8; ++e) av[e] = (f16)(float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
         }
-        f16x8 pb;
-        const int kb = ks >> 1;
-        const int j0 = 4 * (ks & 1);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const f16x2 pr = __builtin_bit_cast(f16x2, p16[kb][j0 + j]);
-          pb[2 * j] = pr[0];
-          pb[2 * j + 1] = pr[1];
-        }
+        const f16x8 pb = __builtin_bit_cast(f16x8, pv[ks]);
         acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb, acc[db], 0, 0, 0);
       }
     }
   }
 
   // ---- epilogue: out = fp16(acc / l) --------------------------------------
+  {
+    const float2 sw = swap_halves(l_i);
+    l_i = sw.x + sw.y;
+  }
   if (row_ok) {
     f16* op = a.out + (int64_t)(q_start + row) * a.so_t + (int64_t)h * a.so_h;
 #pragma unroll
@@ -579,8 +457,5 @@ attn_fwd_kernel(const AttnKArgs a) {
   }
 }
 
-// Launch one instantiation (defined in attn_inst_*.hip).
-void dispatch_attn(const AttnKArgs& a, int nw, int dp, int mode, bool int8v, bool dump, bool bias,
-                   hipStream_t stream);
 
 }  // namespace tmx
