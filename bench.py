@@ -41,7 +41,7 @@ B, HQ, HK, L, D = 8, 24, 8, 4096, 128
 OUTLIER_CHANNELS = (7, 33, 70, 101)
 OUTLIER_SCALE = 8.0
 SEED = 0
-PROFILE_TRAFFIC = REPO / "profiles" / "attn_fwd_cfg2_sptrans50_pmc.txt"
+PROFILE_TRAFFIC = REPO / "profiles" / "attn32_kernel_cfg2_sptrans50_pmc.txt"
 
 
 def algorithmic_ops(b=B, hq=HQ, d=D, l=L) -> float:
@@ -278,7 +278,7 @@ def main() -> int:
             "unit": "TFLOP/s",
             "frac": achieved / peak,
             "traffic": traffic,
-            "kernel": "attn_fwd_kernel<4,128,mixed>",
+            "kernel": "tmx::attn32_kernel<4,128,mixed> (block_m 128, 4 waves x 32 rows)",
             "kernel_ms": k_ms,
             "peak_note": "blended: ops / ((PV + (1-f) QK)/2516.6T + f QK/5033.2T), f = INT8 tile fraction",
         },
