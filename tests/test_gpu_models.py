@@ -1,0 +1,110 @@
+"""GPU tests of the model glue: small random-init Llama / Qwen2 models with
+TileMix injected (SpTrans routing), against the same models whose attention
+call is answered by the CPU oracle (everything else identical, on the GPU).
+
+Bar: top-1 of the logits agrees on >= 99.9% of
+positions; logits stay within a small absolute distance.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
+
+from oracle import tilemix_oracle as O
+from tilemix_amd.models import tilemix_llama as TL
+from tilemix_amd.models import tilemix_qwen as TQ
+
+pytestmark = pytest.mark.gpu
+
+
+def _oracle_varlen_attention(q, k, v, block_m, block_n, *, block_n_mask=None, causal, scale, precision_map_all,
+                             candidates=None, flat_lengths=None, bias=None):
+    """tilemix_varlen_attention computed by the CPU oracle (mixed routing,
+    BLKQ 128 / BLKK 64, fp16 V for PV: the defaults of the dense entry)."""
+    B, Hq, T, D = q.shape
+    Hk = k.shape[1]
+    qn = q.permute(0, 2, 1, 3).reshape(B * T, Hq, D).float().cpu().numpy().astype(np.float16)
+    kn = k.permute(0, 2, 1, 3).reshape(B * T, Hk, D).float().cpu().numpy().astype(np.float16)
+    vn = v.permute(0, 2, 1, 3).reshape(B * T, Hk, D).float().cpu().numpy().astype(np.float16)
+    cu = np.arange(0, (B + 1) * T, T)
+    q8, sq, cuq = O.quant_per_block_int8(qn, cu, 128)
+    k8, sk, cuk = O.quant_per_block_int8(kn, cu, 64)
+    bits = np.array([int(x) for x in precision_map_all.reshape(-1).tolist()], dtype=np.uint64)
+    out = O.attn_fwd(qn, kn, vn, cu, cu, bits, block_m=block_m, block_n_mask=block_n_mask or block_n,
+                     causal=causal, sm_scale=scale, q8=q8, k8=k8, sq16=sq.astype(np.float16),
+                     sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk)
+    o = torch.from_numpy(out.astype(np.float32)).to(q.device, torch.float16)
+    return o.view(B, T, Hq, D).permute(0, 2, 1, 3)
+
+
+def _compare(model, module, ids, monkeypatch):
+    with torch.no_grad():
+        got = model(ids).logits.float()
+        monkeypatch.setattr(module, "tilemix_varlen_attention", _oracle_varlen_attention)
+        ref = model(ids).logits.float()
+        monkeypatch.undo()
+    assert torch.isfinite(got).all()
+    agree = (got.argmax(-1) == ref.argmax(-1)).float().mean().item()
+    diff = (got - ref).abs()
+    return agree, diff.max().item(), diff.mean().item()
+
+
+def test_llama_tilemix_matches_oracle_attention(device, monkeypatch):
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, rope_theta=500000.0)
+    torch.manual_seed(0)
+    model = LlamaForCausalLM(cfg).half().to(device).eval()
+    TL.inject_tilemix_into_llama(model)
+    TL.configure_tilemix_attention_pattern(model, "sptrans", percentage=0.5, stride=128, c=32)
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, 512, (4, 384), generator=g).to(device)
+    agree, dmax, dmean = _compare(model, TL, ids, monkeypatch)
+    assert agree >= 0.999, agree
+    assert dmax < 0.05 and dmean < 2e-3, (dmax, dmean)
+
+
+def test_llama_prefill_helpers_keep_logits(device):
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2)
+    torch.manual_seed(2)
+    model = LlamaForCausalLM(cfg).half().to(device).eval()
+    TL.inject_tilemix_into_llama(model)
+    TL.configure_tilemix_attention_pattern(model, "sptrans", percentage=0.5, stride=64, c=16)
+    ids = torch.randint(0, 512, (2, 256), generator=torch.Generator().manual_seed(3)).to(device)
+    with torch.no_grad():
+        base = model(ids).logits.float()
+        TL.prepare_llama_prefill(model)
+        cache = TL.PrefillCache()
+        out = model(ids, past_key_values=cache, use_cache=True, logits_to_keep=1)
+        fast = out.logits.float()
+    assert cache.get_seq_length(0) == 256
+    assert (fast[:, -1] - base[:, -1]).abs().max().item() < 2e-2
+    assert torch.equal(fast[:, -1].argmax(-1), base[:, -1].argmax(-1))
+
+
+def test_qwen_tilemix_matches_oracle_attention(device, monkeypatch):
+    cfg = Qwen2Config(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=1)
+    torch.manual_seed(4)
+    model = Qwen2ForCausalLM(cfg).half().to(device).eval()
+    TQ.inject_tilemix_into_qwen(model)
+    TQ.configure_tilemix_attention_pattern(model, "bigbird", percentage=0.5)
+    ids = torch.randint(0, 512, (2, 320), generator=torch.Generator().manual_seed(5)).to(device)
+    agree, dmax, dmean = _compare(model, TQ, ids, monkeypatch)
+    assert agree >= 0.999, agree
+    assert dmax < 0.05 and dmean < 2e-3, (dmax, dmean)
+
+
+def test_short_sequences_use_the_parent_attention(device):
+    cfg = LlamaConfig(vocab_size=128, hidden_size=128, intermediate_size=256, num_hidden_layers=1,
+                      num_attention_heads=2, num_key_value_heads=1)
+    torch.manual_seed(6)
+    model = LlamaForCausalLM(cfg).half().to(device).eval()
+    ids = torch.randint(0, 128, (1, 9)).to(device)
+    with torch.no_grad():
+        want = model(ids).logits
+        TL.inject_tilemix_into_llama(model)
+        got = model(ids).logits
+    assert torch.equal(got, want)
