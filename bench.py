@@ -13,9 +13,10 @@ Printed: one JSON line.  ``value`` is effective TOPS of the whole step
 attention kernel alone, timed with HIP events on the launch stream, against
 the blended fp16/int8 MFMA roofline of the routed tile mix; ``cpu_baseline``
 times the CPU oracle (numpy fp32 emulation) on a bounded slice of the same
-workload on this host.
+workload on this host; ``extra.e2e_prefill_ms`` is BASELINE configs[4] (random-
+init fp16 Llama-3.2-3B prefill, B=8 x 4096, TileMix SpTrans50 in every layer).
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--sweep]
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-e2e] [--sweep]
 """
 from __future__ import annotations
 
@@ -124,6 +125,46 @@ def read_traffic():
     return float(m.group(1)) if m else None
 
 
+def e2e_prefill(device, runs: int = 20, warmup: int = 5, seed: int = 0):
+    """random-init fp16 Llama-3.2-3B (28 layers, hidden 3072,
+    24/8 heads, head_dim 128, SwiGLU 8192, vocab 128256, RoPE theta 500000),
+    TileMix injected in every layer with SpTrans p=0.5, prefill helpers on,
+    batch 8 x 4096 seeded token ids into a PrefillCache, last-position logits
+    only.  Returns (median ms, ms of every run)."""
+    import torch
+    from transformers import LlamaConfig, LlamaForCausalLM
+    from tilemix_amd.models import tilemix_llama as TL
+
+    cfg = LlamaConfig(vocab_size=128256, hidden_size=3072, intermediate_size=8192, num_hidden_layers=28,
+                      num_attention_heads=24, num_key_value_heads=8, head_dim=128, rope_theta=500000.0,
+                      max_position_embeddings=131072, rms_norm_eps=1e-5, hidden_act="silu",
+                      tie_word_embeddings=True)
+    torch.manual_seed(seed)
+    with torch.device(device):
+        model = LlamaForCausalLM._from_config(cfg, dtype=torch.float16).eval()
+    TL.inject_tilemix_into_llama(model)
+    TL.configure_tilemix_attention_pattern(model, "sptrans", percentage=0.5, stride=128, c=32)
+    TL.prepare_llama_prefill(model)
+    g = torch.Generator().manual_seed(seed)
+    ids = torch.randint(100, cfg.vocab_size, (B, L), generator=g).to(device)
+    times = []
+    with torch.no_grad():
+        for i in range(warmup + runs):
+            start = torch.cuda.Event(enable_timing=True)
+            end = torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            start.record()
+            out = model(ids, past_key_values=TL.PrefillCache(), use_cache=True, logits_to_keep=1)
+            end.record()
+            torch.cuda.synchronize()
+            if i >= warmup:
+                times.append(start.elapsed_time(end))
+            del out
+    del model
+    torch.cuda.empty_cache()
+    return statistics.median(times), times
+
+
 def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 1):
     """Oracle (numpy fp32 emulation) on sequence 0, the first `sample_groups`
     KV groups (3 query heads each), quantisation included; scaled to TOPS."""
@@ -164,6 +205,7 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-e2e", action="store_true", help="skip the e2e Llama-3.2-3B prefill timing")
     ap.add_argument("--sweep", action="store_true", help="also time SpTrans p in {0,.25,.5,.75,1}")
     ap.add_argument("--kernel-only", type=int, default=0, metavar="N",
                     help="profiling mode: launch only the SpTrans50 attention kernel N times, print nothing else")
@@ -245,6 +287,10 @@ def main() -> int:
             sweep[str(p)] = {"int8_fraction": fp, "step_ms": sp, "kernel_ms": kp,
                              "kernel_roofline_frac": roofline_seconds(fp, ops) / (kp * 1e-3)}
 
+    e2e_ms = None
+    if not args.no_e2e:
+        e2e_ms, _ = e2e_prefill(device)
+
     cpu = None
     if not args.no_cpu:
         cpu = cpu_baseline(q, k, v, row50)
@@ -291,7 +337,8 @@ def main() -> int:
             "speedup_vs_all_fp16_map_step": ms_fp16map / ms,
             "quant_plus_launch_ms": ms - k_ms,
             "sweep": sweep,
-            "e2e_prefill_ms": None,
+            "e2e_prefill_ms": e2e_ms,
+            "e2e_note": "median of 20 after 5 warmups, random-init fp16 Llama-3.2-3B, B8 x 4096, SpTrans50, logits_to_keep=1",
         },
     }
     print(json.dumps(line), flush=True)
