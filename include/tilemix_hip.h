@@ -33,7 +33,7 @@
 extern "C" {
 #endif
 
-#define TILEMIX_ABI_VERSION 1
+#define TILEMIX_ABI_VERSION 2
 
 enum tilemix_status {
     TILEMIX_OK = 0,
@@ -95,6 +95,13 @@ int tilemix_quant_per_block_int8(const tilemix_quant_params* p, void* stream);
  * tile group (block_n_mask keys) to FP16 or INT8 QK^T by bit j of
  * precision_bitmask[hk * ceil(Lq_z / block_m) + m] (hk = h / (heads_q/heads_k)).
  *
+ * q_quant_in_kernel = 1 (block_m == blkq == 128, routing not FP16): each
+ * workgroup quantises its own 128-row Q block (scale = max|q|/127, code =
+ * trunc(q/scale +- 0.5), exactly quant_per_block_int8 with sm_scale = 1, the
+ * way tilemix_attention_with_quant quantises Q, tilemix.py:126-140) instead of
+ * reading q8/sq/cu_q_scale, which may then be NULL.  This removes the Q
+ * pre-pass of tilemix_attention_with_quant; the reference has no such field.
+ *
  * Supported by this build: block_m in {64, 128}; block_n == 64;
  * block_n_mask a multiple of 64 with ceil(max_seqlen_k/block_n_mask) <= 64;
  * head_dim a multiple of 16, <= 128; blkk a multiple of 64; fp16 data.
@@ -133,6 +140,7 @@ typedef struct tilemix_attn_params {
     int32_t causal;
     int32_t routing_mode;         /* enum tilemix_routing_mode                     */
     int32_t int8_use_fp16_v;      /* 1: INT8 tiles use fp16 V for PV (hot path)    */
+    int32_t q_quant_in_kernel;    /* 1: quantise Q inside the attention kernel      */
 } tilemix_attn_params;
 
 int tilemix_attn_fwd(const tilemix_attn_params* p, void* stream);

@@ -258,3 +258,41 @@ def test_varlen_dense_entry(device):
                      sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk)
     got = out.permute(0, 2, 1, 3).reshape(B * T, Hq, D).cpu().numpy()
     assert_close_out(got, ref)
+
+
+# ------------------------------------------- in-kernel Q quantisation (block_m 128)
+FUSED_CASES = [c for c in ATTN_CASES if c[5] == 128 and c[8] != "fp16"]
+
+
+@pytest.mark.parametrize("case", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
+def test_in_kernel_q_quant_bitexact(device, case, monkeypatch):
+    """Q quantised inside the attention kernel gives the oracle's codes and
+    scales exactly: the int32 accumulators match the oracle's integer GEMM of
+    the oracle's codes, and the output equals the pre-pass path bit for bit."""
+    name, lengths, hq, hk, d, block_m, bnm, causal, mode, int8v, kind = case
+    q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=31, outliers=(1, 9))
+    max_len = max(lengths)
+    bits = _bitmask_for(kind, lengths, hk, block_m, bnm, 31)
+    q8, sq, cuq, k8, sk, cuk = oracle_quant(q, k, cu)
+    dq, dk, dv, dcu = (to_dev(x, device) for x in (q, k, v, cu))
+    kw = dict(q8=to_dev(q8, device), k8=to_dev(k8, device), sQ_blocks=to_dev(sq.astype(np.float16), device),
+              sK_blocks=to_dev(sk.astype(np.float16), device), cu_q_scale=to_dev(cuq.astype(np.int32), device),
+              cu_k_scale=to_dev(cuk.astype(np.int32), device), block_m=block_m, block_n_mask=bnm, causal=causal,
+              routing_mode=mode)
+    o_pre, i_pre, f_pre = tmx.debug_launch(dq, dk, dv, dcu, dcu, max_len, max_len, bitmask_tensor(bits, device), **kw)
+    o_fus, i_fus, f_fus = tmx.debug_launch(dq, dk, dv, dcu, dcu, max_len, max_len, bitmask_tensor(bits, device),
+                                           q_in_kernel=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(i_pre, i_fus)
+    assert torch.equal(f_pre.view(torch.int16), f_fus.view(torch.int16))
+    assert torch.equal(o_pre, o_fus)
+    # the public entry: fused (default) vs pre-pass path
+    args = (dq, dk, dv, dcu, dcu, max_len, max_len, bitmask_tensor(bits, device))
+    ekw = dict(block_m=block_m, block_n=64, block_n_mask=bnm, BLKQ=128, BLKK=64, causal=causal,
+               routing_mode=mode, int8_use_fp16_v=int8v)
+    monkeypatch.setenv("TILEMIX_HIP_FUSED_Q_QUANT", "0")
+    out_pre, _ = tmx.tilemix_attention_with_quant(*args, **ekw)
+    monkeypatch.setenv("TILEMIX_HIP_FUSED_Q_QUANT", "1")
+    out_fus, _ = tmx.tilemix_attention_with_quant(*args, **ekw)
+    torch.cuda.synchronize()
+    assert torch.equal(out_pre, out_fus)

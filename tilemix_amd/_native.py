@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libtilemix_hip.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 ROUTING_MIXED = 0
 ROUTING_FP16 = 1
@@ -77,6 +77,7 @@ class AttnParams(ctypes.Structure):
         ("causal", _i32),
         ("routing_mode", _i32),
         ("int8_use_fp16_v", _i32),
+        ("q_quant_in_kernel", _i32),
     ]
 
 

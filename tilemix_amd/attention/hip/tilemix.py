@@ -198,8 +198,13 @@ def launch_prequantized(
     bias: Optional[torch.Tensor] = None, o: Optional[torch.Tensor] = None,
     routing_mode: RoutingMode = "auto", run_length: bool = False,
     scalar_scales: bool = True, int8_cache_ca: bool = False, int8_use_fp16_v: bool = False,
+    _q_in_kernel: bool = False,
 ) -> tuple[torch.Tensor, Literal["mixed", "fp16", "int8"]]:
-    """Reference attention/triton/tilemix.py:1132-1337: validate, then one kernel launch."""
+    """Reference attention/triton/tilemix.py:1132-1337: validate, then one kernel launch.
+
+    ``_q_in_kernel`` (not in the reference): q8 / sQ_blocks / cu_q_scale may be
+    None and the kernel quantises Q itself (block_m == BLKQ == 128 only).
+    """
     if not q.is_cuda:
         raise RuntimeError("TileMix is a GPU-only HIP kernel")
     if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
@@ -238,10 +243,16 @@ def launch_prequantized(
     mode_code = _routing_mode_code(normalized_mode)
 
     quant_tensors = (q8, k8, v8, sQ_blocks, sK_blocks, sV_blocks, cu_q_scale, cu_k_scale, cu_v_scale)
-    if any(t.device != q.device for t in quant_tensors):
+    if any(t is not None and t.device != q.device for t in quant_tensors):
         raise ValueError("all quantization tensors must share q.device")
-    if q8.dtype != torch.int8 or k8.dtype != torch.int8:
+    if (q8 is not None and q8.dtype != torch.int8) or k8.dtype != torch.int8:
         raise TypeError("q8 and k8 must be torch.int8")
+    q_in_kernel = bool(_q_in_kernel) and mode_code != ROUTING_MODE_FP16
+    if q_in_kernel and (block_m != 128 or BLKQ != 128):
+        raise ValueError("in-kernel Q quantisation needs block_m == BLKQ == 128")
+    if mode_code != ROUTING_MODE_FP16 and not q_in_kernel and (q8 is None or sQ_blocks is None
+                                                                or cu_q_scale is None):
+        raise ValueError("q8, sQ_blocks and cu_q_scale are required")
     if v8.dtype != torch.int8:
         raise TypeError("v8 must be torch.int8")
 
@@ -290,17 +301,20 @@ def launch_prequantized(
     p.stride_o_token, p.stride_o_head = o_dev.stride(0), o_dev.stride(1)
     keep = []
     if mode_code != ROUTING_MODE_FP16:
-        q8c = _inner_contiguous(q8, 16)
+        if q_in_kernel:
+            p.q_quant_in_kernel = 1
+        else:
+            q8c = _inner_contiguous(q8, 16)
+            sq = sQ_blocks.to(torch.float16).contiguous()
+            cqs = cu_q_scale.to(dtype=torch.int32).contiguous()
+            keep += [q8c, sq, cqs]
+            p.q8, p.sq, p.cu_q_scale = q8c.data_ptr(), sq.data_ptr(), cqs.data_ptr()
+            p.stride_q8_token, p.stride_q8_head = q8c.stride(0), q8c.stride(1)
         k8c = _inner_contiguous(k8, 16)
-        sq = sQ_blocks.to(torch.float16).contiguous()
         sk = sK_blocks.to(torch.float16).contiguous()
-        cqs = cu_q_scale.to(dtype=torch.int32).contiguous()
         cks = cu_k_scale.to(dtype=torch.int32).contiguous()
-        keep += [q8c, k8c, sq, sk, cqs, cks]
-        p.q8, p.k8 = q8c.data_ptr(), k8c.data_ptr()
-        p.sq, p.sk = sq.data_ptr(), sk.data_ptr()
-        p.cu_q_scale, p.cu_k_scale = cqs.data_ptr(), cks.data_ptr()
-        p.stride_q8_token, p.stride_q8_head = q8c.stride(0), q8c.stride(1)
+        keep += [k8c, sk, cks]
+        p.k8, p.sk, p.cu_k_scale = k8c.data_ptr(), sk.data_ptr(), cks.data_ptr()
         p.stride_k8_token, p.stride_k8_head = k8c.stride(0), k8c.stride(1)
         if not int8_use_fp16_v:
             v8c = _inner_contiguous(v8, 8)
@@ -364,7 +378,11 @@ def tilemix_attention_with_quant(
     else:
         if not q.is_cuda:
             raise RuntimeError("TileMix is a GPU-only HIP kernel")
-        q8, sq, cuq = _quantize_for_launch(q, cu_seqlens_q, max_seqlens_q, BLKQ)
+        fused = _q_in_kernel_enabled() and block_m == 128 and BLKQ == 128
+        if fused:
+            q8 = sq = cuq = None
+        else:
+            q8, sq, cuq = _quantize_for_launch(q, cu_seqlens_q, max_seqlens_q, BLKQ)
         k8, sk, cuk = _quantize_for_launch(k, cu_seqlens_k, max_seqlens_k, BLKK)
         if int8_use_fp16_v:
             v8, sv, cuv = _dummy_v_quantization_metadata(v, cu_seqlens_k)
@@ -373,6 +391,7 @@ def tilemix_attention_with_quant(
         quantized = q8, sq, cuq, k8, sk, cuk, v8, sv, cuv
 
     q8, sq, cuq, k8, sk, cuk, v8, sv, cuv = quantized
+    fused = normalized_mode != "fp16" and q8 is None
     return launch_prequantized(
         q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlens_q, max_seqlens_k, precision_bitmask,
         q8=q8, k8=k8, v8=v8, sQ_blocks=sq, sK_blocks=sk, sV_blocks=sv,
@@ -380,19 +399,27 @@ def tilemix_attention_with_quant(
         block_m=block_m, block_n=block_n, block_n_mask=block_n_mask, BLKQ=BLKQ, BLKK=BLKK,
         causal=causal, sm_scale=sm_scale, bias=bias, routing_mode=normalized_mode,
         run_length=run_length, scalar_scales=scalar_scales, int8_cache_ca=int8_cache_ca,
-        int8_use_fp16_v=int8_use_fp16_v,
+        int8_use_fp16_v=int8_use_fp16_v, _q_in_kernel=fused,
     )
+
+
+def _q_in_kernel_enabled() -> bool:
+    """``TILEMIX_HIP_FUSED_Q_QUANT`` (default 1): with block_m == BLKQ == 128 the
+    attention kernel quantises Q itself instead of a separate pre-pass (same
+    codes and scales, bit for bit)."""
+    return os.environ.get("TILEMIX_HIP_FUSED_Q_QUANT", "1").strip() not in ("0", "false", "False", "")
 
 
 def debug_launch(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlens_q, max_seqlens_k, precision_bitmask,
                  *, q8, k8, sQ_blocks, sK_blocks, cu_q_scale, cu_k_scale, block_m, block_n_mask,
-                 BLKQ=128, BLKK=64, causal=True, sm_scale=None, routing_mode="mixed"):
+                 BLKQ=128, BLKK=64, causal=True, sm_scale=None, routing_mode="mixed", q_in_kernel=False):
     """Run the kernel's DUMP instantiation (C entry ``tilemix_attn_fwd_debug``).
 
     Returns ``(out, qk_i32 [tokens_q, Hq, max_k] int32, qk16 [tokens_q, Hq, max_k] fp16)``;
     entries the kernel did not compute keep the fill values (INT32_MIN / NaN).
     No reference counterpart: it exposes the int32 Q8.K8 accumulators and the
-    fp16 scores for the bit-exact parity tests.
+    fp16 scores for the bit-exact parity tests.  ``q_in_kernel``: the kernel
+    quantises Q itself (q8 / sQ_blocks / cu_q_scale are then ignored).
     """
     mode_code = _routing_mode_code(routing_mode)
     device = q.device
@@ -430,5 +457,6 @@ def debug_launch(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlens_q, max_seqlens
     p.causal = 1 if causal else 0
     p.routing_mode = mode_code
     p.int8_use_fp16_v = 1
+    p.q_quant_in_kernel = 1 if q_in_kernel else 0
     _native.attn_fwd_debug(p, qk_i32, qk16, device)
     return o, qk_i32, qk16

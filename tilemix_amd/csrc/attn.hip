@@ -61,8 +61,18 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   }
   // Tiles are streamed as 16-byte vectors: 16-byte aligned bases and strides.
   if (need_int8) {
-    if (!p.q8 || !p.k8 || !p.sq || !p.sk || !p.cu_q_scale || !p.cu_k_scale) {
-      set_error("%s: int8 routing needs q8/k8/sq/sk/cu_q_scale/cu_k_scale", fn);
+    if (p.q_quant_in_kernel) {
+      if (p.block_m != 128 || p.blkq != 128) {
+        set_error("%s: q_quant_in_kernel needs block_m == BLKQ == 128 (block_m=%d, BLKQ=%d)", fn, p.block_m,
+                  p.blkq);
+        return TILEMIX_E_INVALID;
+      }
+    } else if (!p.q8 || !p.sq || !p.cu_q_scale) {
+      set_error("%s: int8 routing needs q8/sq/cu_q_scale (or q_quant_in_kernel)", fn);
+      return TILEMIX_E_INVALID;
+    }
+    if (!p.k8 || !p.sk || !p.cu_k_scale) {
+      set_error("%s: int8 routing needs k8/sk/cu_k_scale", fn);
       return TILEMIX_E_INVALID;
     }
     if (p.blkq <= 0 || p.blkk <= 0 || p.blkk % kBN != 0) {
@@ -70,8 +80,8 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
                 p.blkq, p.blkk);
       return TILEMIX_E_INVALID;
     }
-    if (!aligned(p.q8, 16) || !aligned(p.k8, 16) || (p.stride_q8_token | p.stride_q8_head) % 16 ||
-        (p.stride_k8_token | p.stride_k8_head) % 16) {
+    const bool q8_bad = !p.q_quant_in_kernel && (!aligned(p.q8, 16) || (p.stride_q8_token | p.stride_q8_head) % 16);
+    if (q8_bad || !aligned(p.k8, 16) || (p.stride_k8_token | p.stride_k8_head) % 16) {
       set_error("%s: q8/k8 must be 16-byte aligned with strides multiple of 16 elements", fn);
       return TILEMIX_E_INVALID;
     }
@@ -168,6 +178,7 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.blkq = p.blkq > 0 ? p.blkq : 1;
   a.blkk = p.blkk > 0 ? p.blkk : kBN;
   a.causal = p.causal ? 1 : 0;
+  a.q_fused = (need_int8 && p.q_quant_in_kernel) ? 1 : 0;
   const bool dump = dump_i32 != nullptr || dump_f16 != nullptr;
   a.total_items = (int)total;
   a.per_xcd = (int)((total + 7) / 8);

@@ -40,6 +40,7 @@ struct AttnKArgs {
   int mask_tiles; // block_n_mask / block_n
   int blkq, blkk;
   int causal;
+  int q_fused;      // Q quantised in the attention kernel (block_m == BLKQ == 128)
   int total_items;  // (sequence, query head, query block) work items
   int per_xcd;
 };
@@ -84,6 +85,17 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   v[0] = (f16)a;
   v[1] = (f16)b;
   return __builtin_bit_cast(uint32_t, v);
+}
+
+// x / s correctly rounded, from r = RN(1/s): q0 = RN(x r), rem = x - q0 s
+// (exact, one FMA), RN(q0 + rem r) (Markstein's correction step).  For the
+// quantisation domain (x an fp16 value, s = RN(amax/127) with |x| <= amax, amax
+// a positive fp16 value) this equals IEEE x / s on all 1.0e9 (x, amax) pairs
+// up to the sign of a zero quotient, which the int8 code does not see.
+__device__ __forceinline__ float div_by_recip(float x, float s, float r) {
+  const float q0 = x * r;
+  const float rem = __builtin_fmaf(-q0, s, x);
+  return __builtin_fmaf(rem, r, q0);
 }
 
 // Lane pairs (l, l^16) and (l, l^32): returns {value of the lower lane, value

@@ -12,7 +12,7 @@
 // kRegChunks * 256 eight-element chunks (BLK * D <= 16384: every Q/K block of
 // the hot path) are read from HBM once and held in registers between the max
 // pass and the code pass; larger blocks are streamed twice.
-#include "common.h"
+#include "attn_common.h"
 
 namespace tmx {
 
@@ -81,11 +81,15 @@ __global__ void __launch_bounds__(kQuantThreads) quant_per_block_int8_kernel(con
   int8_t* out = a.out + tok0 * a.so_t + (int64_t)h * a.so_h;
 
   const float sm = a.sm_scale;
-  auto encode = [&](const f16x8& x, float s, int r, int col) {
+  // sm_scale == 1 (the hot path: quantize_q(k)_for_tilemix): the quotient is
+  // taken from an IEEE reciprocal with one correction step, equal to the IEEE
+  // division on the whole fp16 domain; other scales divide directly.
+  const bool unit_scale = sm == 1.0f;
+  auto encode = [&](const f16x8& x, float s, float rs, int r, int col) {
     uint32_t w0 = 0, w1 = 0;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      float t = ((float)x[e] * sm) / s;
+      float t = unit_scale ? div_by_recip((float)x[e], s, rs) : ((float)x[e] * sm) / s;
       t += (t >= 0.0f) ? 0.5f : -0.5f;
       // An all-zero block gives 0/0; its codes are defined as 0.
       const int code = (s == 0.0f) ? 0 : (int)t;
@@ -120,12 +124,13 @@ __global__ void __launch_bounds__(kQuantThreads) quant_per_block_int8_kernel(con
       }
     }
     s = block_max(amax) / 127.0f;  // IEEE division (no fast-math in this build)
+    const float rs = 1.0f / s;
 #pragma unroll
     for (int i = 0; i < kRegChunks; ++i) {
       const int c = tid + i * kQuantThreads;
       if (c < chunks) {
         const int r = c / cpr, col = (c - r * cpr) << 3;
-        encode(xs[i], s, r, col);
+        encode(xs[i], s, rs, r, col);
       }
     }
   } else {
@@ -137,9 +142,10 @@ __global__ void __launch_bounds__(kQuantThreads) quant_per_block_int8_kernel(con
       for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf((float)x[e] * sm));
     }
     s = block_max(amax) / 127.0f;
+    const float rs = 1.0f / s;
     for (int c = tid; c < chunks; c += kQuantThreads) {
       const int r = c / cpr, col = (c - r * cpr) << 3;
-      encode(*reinterpret_cast<const f16x8*>(in + (int64_t)r * a.si_t + col), s, r, col);
+      encode(*reinterpret_cast<const f16x8*>(in + (int64_t)r * a.si_t + col), s, rs, r, col);
     }
   }
   if (tid == 0) {
