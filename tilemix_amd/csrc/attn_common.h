@@ -120,6 +120,38 @@ __device__ __forceinline__ void async_load16(__amdgpu_buffer_rsrc_t rsrc, int vo
   __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds_wave_base, 16, voffset, 0, 0, 0);
 }
 
+// The same HBM -> LDS copy issued from inline assembly, for kernels that
+// order it against their LDS reads themselves (s_waitcnt vmcnt(0) + barrier
+// before a stage is read).  Issued through the builtin, the compiler cannot
+// tell the stage being filled from the stage being read and waits for the
+// copy before every LDS read, which serialises the prefetch with the tile's
+// compute.  rsrc and lds_addr are wave-uniform (SGPRs); M0 carries the LDS
+// address, and one wait state separates its write from the load.
+struct SRsrc {
+  i32x4 w;
+};
+__device__ __forceinline__ SRsrc make_srsrc(const void* base, int bytes) {
+  const uint64_t p = reinterpret_cast<uint64_t>(base);
+  SRsrc r;
+  r.w[0] = __builtin_amdgcn_readfirstlane((int)(uint32_t)p);
+  r.w[1] = __builtin_amdgcn_readfirstlane((int)((p >> 32) & 0xffffu));
+  r.w[2] = __builtin_amdgcn_readfirstlane(bytes);
+  r.w[3] = 0x00020000;
+  return r;
+}
+__device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
+  return (uint32_t)__builtin_amdgcn_readfirstlane(
+      (int)(uint32_t)reinterpret_cast<uintptr_t>((const lds_void*)p));
+}
+__device__ __forceinline__ void async_load16_asm(const SRsrc& rs, int voffset, uint32_t lds) {
+  asm volatile(
+      "s_nop 0\n\t"
+      "buffer_load_dwordx4 %0, %1, 0 offen lds"
+      :
+      : "v"(voffset), "s"(rs.w), "{m0}"(lds)
+      : "memory");
+}
+
 // Transposed LDS reads (gfx950).  tr16: within each 16-lane group, output lane
 // i, element c = element (i % 4) of the 8 bytes addressed by lane 4c + i/4.
 // tr8: output lane i, byte b = byte (i % 8) of the 8 bytes addressed by lane

@@ -190,12 +190,6 @@ attn32_kernel(const AttnKArgs a) {
     }
   }
 
-  auto route_of = [&](int n) -> int {
-    if (MODE == TILEMIX_ROUTING_FP16) return 0;
-    if (MODE == TILEMIX_ROUTING_INT8) return 1;
-    return (int)((bits >> (unsigned)(n / a.mask_tiles)) & 1ull);
-  };
-
   // ---- asynchronous tile loads (HBM -> LDS, no registers) -----------------
   // Each tile is fetched through raw buffers based at the tile's first key
   // and sized to the keys left in the sequence: rows past the end read as 0
@@ -218,31 +212,71 @@ attn32_kernel(const AttnKArgs a) {
     else sw = swz_k<64>(r);
     return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
   };
-  auto issue_tile = [&](int n, int route, unsigned char* stage) {
+  const uint32_t smem_lds = lds_addr(smem);
+  auto issue_tile = [&](int n, int route, uint32_t stage) {
     const int key0 = n * kBN;
     const int rem = Lk - key0;  // >= 1
     if (route == 0) {
-      const auto rs = make_rsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
+      const SRsrc rs = make_srsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
 #pragma unroll
       for (int i = 0; i < K16_INS; ++i)
-        async_load16(rs, lane_off(i, ROW16, kt_bytes, false), stage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, lane_off(i, ROW16, kt_bytes, false), stage + (i * NW + wave) * 1024);
     } else {
-      const auto rs = make_rsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
+      const SRsrc rs = make_srsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
 #pragma unroll
       for (int i = 0; i < K8_INS; ++i)
-        async_load16(rs, lane_off(i, ROW8, k8t_bytes, false), stage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, lane_off(i, ROW8, k8t_bytes, false), stage + (i * NW + wave) * 1024);
     }
-    unsigned char* vstage = stage + KBUF;
+    const uint32_t vstage = stage + KBUF;
     if (!INT8V || route == 0) {
-      const auto rs = make_rsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
+      const SRsrc rs = make_srsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
 #pragma unroll
       for (int i = 0; i < V16_INS; ++i)
-        async_load16(rs, lane_off(i, ROW16, vt_bytes, true), vstage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, lane_off(i, ROW16, vt_bytes, true), vstage + (i * NW + wave) * 1024);
     } else {
-      const auto rs = make_rsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
+      const SRsrc rs = make_srsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
 #pragma unroll
       for (int i = 0; i < V8_INS; ++i)
-        async_load16(rs, lane_off(i, ROW8, v8t_bytes, false), vstage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, lane_off(i, ROW8, v8t_bytes, false), vstage + (i * NW + wave) * 1024);
+    }
+  };
+
+  // Per-tile route bit and K/V scale block, advanced tile by tile (no
+  // divisions in the loop): tile t has route group t / mask_tiles and scale
+  // block key0 / blkk = t / (blkk / 64).
+  const int kb_tiles = a.blkk / kBN;
+  int nx_grp = 0, nx_gc = 0, nx_sb = 0, nx_sc = 0;  // of the next tile to issue
+  int kbase = 0, kend = 0, vbase = 0, vend = 0;
+  if (MODE != TILEMIX_ROUTING_FP16) {
+    kbase = a.cu_ks[z];
+    kend = a.cu_ks[z + 1];
+  }
+  if (INT8V) {
+    vbase = a.cu_vs[z];
+    vend = a.cu_vs[z + 1];
+  }
+  // Issues the next tile (index nx) and fetches its scales; the loads land
+  // before the barrier that precedes the tile's compute.
+  auto issue_next = [&](int nx, uint32_t stage, int& route, f16& skv, f16& svv) {
+    route = MODE == TILEMIX_ROUTING_FP16 ? 0
+          : MODE == TILEMIX_ROUTING_INT8 ? 1
+          : (int)((bits >> (unsigned)nx_grp) & 1ull);
+    issue_tile(nx, route, stage);
+    if (MODE != TILEMIX_ROUTING_FP16 && route == 1) {
+      skv = (f16)1.0f;
+      if (kend > kbase) skv = a.sk[(int64_t)min(kbase + nx_sb, kend - 1) * a.hk + hk];
+      if (INT8V) {
+        svv = (f16)1.0f;
+        if (vend > vbase) svv = a.sv[(int64_t)min(vbase + nx_sb, vend - 1) * a.hk + hk];
+      }
+    }
+    if (++nx_gc == a.mask_tiles) {
+      nx_gc = 0;
+      ++nx_grp;
+    }
+    if (++nx_sc == kb_tiles) {
+      nx_sc = 0;
+      ++nx_sb;
     }
   };
 
@@ -257,27 +291,31 @@ attn32_kernel(const AttnKArgs a) {
 #pragma unroll
   for (int db = 0; db < NDB; ++db) acc[db] = (f32x16){};
 
-  // The magic bias as an MFMA C operand (first k-step of every INT8 tile).
-  const i32x16 kMagicC = {0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000,
-                         0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000,
-                         0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
-  int route_next = 0;
-  if (n_blocks > 0) {
-    route_next = route_of(0);
-    issue_tile(0, route_next, smem);
+  // The magic bias as the MFMA C operand of the first k-step of every INT8
+  // tile, kept in VGPRs for the whole loop (the barrier stops the compiler from
+  // rebuilding the 16 constants before every INT8 tile).
+  i32x16 magic_c;
+#pragma unroll
+  for (int e = 0; e < 16; ++e) {
+    int mv = 0x4B400000;
+    if (MODE != TILEMIX_ROUTING_FP16) asm volatile("" : "+v"(mv));
+    magic_c[e] = mv;
   }
+  int route_next = 0;
+  f16 sk_next = (f16)1.0f, sv_next = (f16)1.0f;
+  if (n_blocks > 0) issue_next(0, smem_lds, route_next, sk_next, sv_next);
 
   for (int n = 0; n < n_blocks; ++n) {
     const int route = route_next;
+    const f16 sk16 = sk_next;
+    const f16 sv16 = sv_next;
     unsigned char* stage = smem + (n & 1) * STAGE;
     // Tile n has landed (own loads), then every wave's loads have landed and
     // every wave is done with the other stage (tile n-1).
     __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
-    if (n + 1 < n_blocks) {
-      route_next = route_of(n + 1);
-      issue_tile(n + 1, route_next, smem + ((n + 1) & 1) * STAGE);
-    }
+    if (n + 1 < n_blocks)
+      issue_next(n + 1, smem_lds + ((n + 1) & 1) * STAGE, route_next, sk_next, sv_next);
 
     const int key0 = n * kBN;
     // Fully masked for this wave (or rows past the sequence end): the
@@ -312,16 +350,10 @@ attn32_kernel(const AttnKArgs a) {
         for (int j = 0; j < 8; ++j) s16[kb][j] = pack_h2(c[2 * j], c[2 * j + 1]);
       }
     } else {
-      f16 sk16 = (f16)1.0f;
-      {
-        const int kbase = a.cu_ks[z], kend = a.cu_ks[z + 1];
-        if (kend > kbase) {
-          const int idx = min(kbase + key0 / a.blkk, kend - 1);
-          sk16 = a.sk[(int64_t)idx * a.hk + hk];
-        }
-      }
       const f16 sqk = sq16 * sk16;
-      const float ss = (float)(f16)fp32_round((float)sqk * a.qk_scale);
+      // ss is fp16-exact; the barrier keeps it an fp32 operand (v_fma_f32
+      // below, not the slower mixed-precision form).
+      const float ss = fp32_round((float)(f16)fp32_round((float)sqk * a.qk_scale));
       // acc is accumulated on top of the integer bits of 1.5*2^23, so
       // float(bits) = 1.5*2^23 + acc exactly (|acc| < 2^22); fma(F, ss,
       // -1.5*2^23*ss) is then the single rounding of acc*ss (1.5*2^23*ss is
@@ -336,7 +368,7 @@ attn32_kernel(const AttnKArgs a) {
         for (int ks = 0; ks < KS8; ++ks) {
           const int ch = (2 * ks + hi) ^ swz_k<ROW8>(r);
           const i32x4 av = *reinterpret_cast<const i32x4*>(stage + r * ROW8 + ch * 16);
-          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], ks == 0 ? kMagicC : c, 0, 0, 0);
+          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], ks == 0 ? magic_c : c, 0, 0, 0);
         }
         if (DUMP && a.dump_i32 != nullptr && row_ok) {
 #pragma unroll
@@ -439,12 +471,6 @@ attn32_kernel(const AttnKArgs a) {
     if (INT8V && route == 1) {
       // Reference :449-497: PV on int8 V codes with p scaled by the V block
       // scale in fp16: p_scaled = fp16(p * sv).
-      f16 sv16 = (f16)1.0f;
-      const int vb = a.cu_vs[z], ve = a.cu_vs[z + 1];
-      if (ve > vb) {
-        const int idx = min(vb + key0 / a.blkk, ve - 1);
-        sv16 = a.sv[(int64_t)idx * a.hk + hk];
-      }
       const f16x8 sv8 = {sv16, sv16, sv16, sv16, sv16, sv16, sv16, sv16};
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) pv[ks] = __builtin_bit_cast(u32x4, __builtin_bit_cast(f16x8, pv[ks]) * sv8);
