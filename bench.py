@@ -211,6 +211,8 @@ def main() -> int:
                     help="profiling mode: launch only the SpTrans50 attention kernel N times, print nothing else")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="profiling mode: one device copy of MIB MiB (HBM counter calibration)")
+    ap.add_argument("--e2e-only", type=int, default=0, metavar="N",
+                    help="profiling mode: only the e2e Llama-3.2-3B prefill, N timed runs after 1 warmup")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one MI355X: the TileMix prefill path shards with no exchange "
@@ -231,6 +233,10 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         print(f"copied {args.copy_calibration} MiB", flush=True)
+        return 0
+    if args.e2e_only:
+        med, times = e2e_prefill(device, runs=args.e2e_only, warmup=1)
+        print(f"e2e prefill median {med:.2f} ms over {len(times)} runs", flush=True)
         return 0
     q, k, v = make_inputs(device)
     cu = torch.arange(0, (B + 1) * L, L, dtype=torch.int32, device=device)

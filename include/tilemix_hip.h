@@ -11,6 +11,10 @@
  *       attention/triton/tilemix.py:503-579 (kernel signature)
  *       attention/triton/tilemix.py:1286-1336 (launch site in launch_prequantized)
  *
+ * and the three prefill helper kernels of the LLaMA glue
+ * (models/tilemix_llama.py:718-869: squared-mean RMSNorm, token-major rotary,
+ * SiLU * up).
+ *
  * Conventions (all entry points):
  *   - Plain C types only: device pointers, element strides, sizes.  No torch
  *     types cross this boundary.  `stream` is a hipStream_t passed as void*
@@ -33,7 +37,7 @@
 extern "C" {
 #endif
 
-#define TILEMIX_ABI_VERSION 2
+#define TILEMIX_ABI_VERSION 3
 
 enum tilemix_status {
     TILEMIX_OK = 0,
@@ -164,9 +168,66 @@ int tilemix_attn_fwd_debug(const tilemix_attn_params* p,
                            int64_t dump_stride_token, int64_t dump_stride_head,
                            void* stream);
 
+/*
+ * Prefill helpers of the LLaMA glue (all fp16 in / fp16 out, fp32 arithmetic).
+ *
+ * RMSNorm.  Replaces PrefillRMSNorm.forward (models/tilemix_llama.py:788-797):
+ * the squared_mean extension (:718-760, fp32 mean of x^2 over the last dim)
+ * and _norm_tail (:763-765).  For every row r of `rows` rows of `cols` values:
+ *   var      = (sum_c fp32(x)^2) * fp32(1 / cols)
+ *   out[r,c] = fp16( fp32(w[c]) * fp32( fp16( fp32(x[r,c]) * rsqrt(var + eps) ) ) )
+ * Rows are `stride_x` / `stride_out` elements apart; the last dim is contiguous.
+ */
+typedef struct tilemix_rmsnorm_params {
+    const void* x;                /* fp16 [rows, cols] (row stride stride_x)       */
+    const void* weight;           /* fp16 [cols]                                   */
+    void* out;                    /* fp16 [rows, cols] (row stride stride_out)     */
+    int64_t rows;
+    int64_t stride_x, stride_out;
+    int32_t cols;
+    float eps;
+} tilemix_rmsnorm_params;
+
+int tilemix_rms_norm_f16(const tilemix_rmsnorm_params* p, void* stream);
+
+/*
+ * Split-half rotary embedding of Q and K into token-major outputs.
+ * Replaces the _rotary Triton kernel and its launch in rotary_token_major
+ * (models/tilemix_llama.py:808-847).  For batch b, token t, head h, dim d
+ * (D = head_dim, d' = (d + D/2) % D, sign = -1 for d < D/2 else +1):
+ *   out[b,t,h,d] = fp16( fp32(fp16(x[b,h,t,d] * c)) + fp32(fp16(x[b,h,t,d'] * sign * s)) )
+ * with c = cos[b,t,d], s = sin[b,t,d] (batch stride 0 broadcasts one row);
+ * q_out is [batch, tokens, heads_q, D], k_out [batch, tokens, heads_k, D],
+ * both contiguous.  Input strides are in elements; the dim stride is 1.
+ */
+typedef struct tilemix_rotary_params {
+    const void* q;                /* fp16 [batch, heads_q, tokens, D] (strided)    */
+    const void* k;                /* fp16 [batch, heads_k, tokens, D] (strided)    */
+    const void* cos;              /* fp16 [batch or 1, tokens, D] (strided)        */
+    const void* sin;
+    void* q_out;                  /* fp16 [batch, tokens, heads_q, D] contiguous   */
+    void* k_out;                  /* fp16 [batch, tokens, heads_k, D] contiguous   */
+    int64_t stride_q_batch, stride_q_head, stride_q_token;
+    int64_t stride_k_batch, stride_k_head, stride_k_token;
+    int64_t stride_cos_batch, stride_cos_token;
+    int64_t stride_sin_batch, stride_sin_token;
+    int32_t batch, tokens, heads_q, heads_k, head_dim;  /* head_dim even          */
+} tilemix_rotary_params;
+
+int tilemix_rotary_f16(const tilemix_rotary_params* p, void* stream);
+
+/*
+ * SiLU(gate) * up.  Replaces the _silu_mul Triton kernel and silu_mul
+ * (models/tilemix_llama.py:850-869):
+ *   out[i] = fp16( fp32( fp16( g / (1 + exp(-g)) ) ) * fp32(up[i]) ),  g = fp32(gate[i])
+ * with an IEEE fp32 division.  gate, up and out are contiguous, n elements.
+ */
+int tilemix_silu_mul_f16(const void* gate, const void* up, void* out, int64_t n, void* stream);
+
 /* Library introspection. */
 int tilemix_abi_version(void);
-/* sizeof() of the parameter structs as compiled into the library: 0 = quant, 1 = attn. */
+/* sizeof() of the parameter structs as compiled into the library:
+ * 0 = quant, 1 = attn, 2 = rmsnorm, 3 = rotary. */
 int64_t tilemix_params_size(int which);
 const char* tilemix_last_error(void);
 

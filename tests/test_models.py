@@ -8,6 +8,7 @@ import torch
 from transformers import LlamaConfig, LlamaForCausalLM, Qwen2Config, Qwen2ForCausalLM
 from transformers.models.llama.modeling_llama import apply_rotary_pos_emb
 
+from oracle import prefill_oracle as PO
 from tilemix_amd.attention import precision_maps as pm
 from tilemix_amd.models import tilemix_llama as TL
 from tilemix_amd.models import tilemix_qwen as TQ
@@ -139,7 +140,9 @@ def test_prefill_cache_keeps_first_update():
     assert cache.get_seq_length(0) == 41
 
 
-def test_rotary_token_major_matches_hf_fp16():
+def test_rotary_oracle_matches_hf_fp16():
+    """The oracle's split-half RoPE (the checker of the HIP kernel) equals
+    transformers' apply_rotary_pos_emb on fp16 tensors bit for bit."""
     torch.manual_seed(1)
     b, hq, hk, t, d = 2, 4, 2, 37, 32
     q = torch.randn(b, hq, t, d).half()
@@ -149,23 +152,60 @@ def test_rotary_token_major_matches_hf_fp16():
     freqs = torch.outer(pos, inv)
     emb = torch.cat((freqs, freqs), dim=-1)
     cos, sin = emb.cos().half()[None].expand(b, t, d).contiguous(), emb.sin().half()[None].expand(b, t, d).contiguous()
-    oq, ok = TL.rotary_token_major(q, k, cos, sin)
+    oq, ok = PO.rotary_token_major(q, k, cos, sin)
     rq, rk = apply_rotary_pos_emb(q, k, cos, sin)
     assert torch.equal(oq, rq) and torch.equal(ok, rk)
     # token-major storage: the [b, h, t, d] view is a transpose of a dense [b, t, h, d]
     assert oq.transpose(1, 2).is_contiguous() and ok.transpose(1, 2).is_contiguous()
+
+
+def test_rotary_product_validates_then_needs_gpu():
+    q = torch.randn(1, 2, 8, 16).half()
+    k = torch.randn(1, 1, 8, 16).half()
+    cos = torch.randn(1, 8, 16).half()
     with pytest.raises(ValueError, match="FP16"):
-        TL.rotary_token_major(q.float(), k, cos, sin)
+        TL.rotary_token_major(q.float(), k, cos, cos)
+    with pytest.raises(ValueError, match="split-half"):
+        TL.rotary_token_major(q, k[..., :8], cos, cos)
+    with pytest.raises(RuntimeError, match="GPU-only HIP kernel"):
+        TL.rotary_token_major(q, k, cos, cos)
 
 
-def test_silu_mul_matches_fp16_reference():
+def test_silu_mul_oracle_matches_fp16_reference():
     torch.manual_seed(2)
     g = (torch.randn(64, 96) * 4).half()
     u = torch.randn(64, 96).half()
     want = (torch.nn.functional.silu(g.float()).half().float() * u.float()).half()
-    assert torch.equal(TL.silu_mul(g, u), want)
+    assert torch.equal(PO.silu_mul(g, u), want)
     with pytest.raises(ValueError, match="equally shaped FP16"):
         TL.silu_mul(g, u[:, :10])
+    with pytest.raises(RuntimeError, match="GPU-only HIP kernel"):
+        TL.silu_mul(g, u)
+
+
+def test_rms_norm_oracle_matches_llama_rmsnorm():
+    """The oracle's RMSNorm equals transformers' LlamaRMSNorm run in fp16 on the
+    CPU bit for bit (same formula and rounding points), and an fp64 evaluation
+    of the formula to one fp16 ulp."""
+    from transformers.models.llama.modeling_llama import LlamaRMSNorm
+    torch.manual_seed(3)
+    x = (torch.randn(33, 200) * 3).half()
+    norm = LlamaRMSNorm(200, eps=1e-5)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(200) * 0.5 + 1.0)
+    norm = norm.half()
+    with torch.no_grad():
+        want = norm(x)
+    got = PO.rms_norm(x, norm.weight.detach(), 1e-5)
+    assert torch.equal(got, want)
+    xd = x.double()
+    exact = norm.weight.double() * (xd / torch.sqrt((xd * xd).mean(-1, keepdim=True) + 1e-5)).half().double()
+    ulp = torch.finfo(torch.float16).eps * exact.abs().clamp_min(2 ** -14)
+    assert ((got.double() - exact).abs() <= ulp + 1e-12).all()
+    with pytest.raises(ValueError, match="FP16"):
+        TL.rms_norm(x.float(), norm.weight, 1e-5)
+    with pytest.raises(RuntimeError, match="GPU-only HIP kernel"):
+        TL.rms_norm(x, norm.weight.detach(), 1e-5)
 
 
 def test_prepare_llama_prefill_checks_and_swaps():
@@ -180,9 +220,8 @@ def test_prepare_llama_prefill_checks_and_swaps():
     layer = model.model.layers[0]
     assert isinstance(layer.mlp, TL.PrefillMLP) and isinstance(layer.input_layernorm, TL.PrefillRMSNorm)
     assert layer.self_attn.apply_rotary is TL.rotary_token_major
-    x = torch.randn(3, 128).half()
-    ref = model.model.norm.weight * (x.float() * torch.rsqrt(x.float().pow(2).mean(-1, keepdim=True) + 1e-6)).half()
-    assert torch.allclose(model.model.norm(x).float(), ref.float(), atol=1e-3)
+    with pytest.raises(RuntimeError, match="GPU-only HIP kernel"):
+        model.model.norm(torch.randn(3, 128).half())
     model.train()
     with pytest.raises(ValueError, match="eval-mode SiLU"):
         TL.prepare_llama_prefill(model)

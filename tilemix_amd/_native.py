@@ -15,7 +15,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().parent / "libtilemix_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 ROUTING_MIXED = 0
 ROUTING_FP16 = 1
@@ -81,10 +81,36 @@ class AttnParams(ctypes.Structure):
     ]
 
 
+class RmsNormParams(ctypes.Structure):
+    """Mirror of ``tilemix_rmsnorm_params``."""
+
+    _fields_ = [
+        ("x", _vp), ("weight", _vp), ("out", _vp),
+        ("rows", _i64), ("stride_x", _i64), ("stride_out", _i64),
+        ("cols", _i32), ("eps", _f32),
+    ]
+
+
+class RotaryParams(ctypes.Structure):
+    """Mirror of ``tilemix_rotary_params``."""
+
+    _fields_ = [
+        ("q", _vp), ("k", _vp), ("cos", _vp), ("sin", _vp), ("q_out", _vp), ("k_out", _vp),
+        ("stride_q_batch", _i64), ("stride_q_head", _i64), ("stride_q_token", _i64),
+        ("stride_k_batch", _i64), ("stride_k_head", _i64), ("stride_k_token", _i64),
+        ("stride_cos_batch", _i64), ("stride_cos_token", _i64),
+        ("stride_sin_batch", _i64), ("stride_sin_token", _i64),
+        ("batch", _i32), ("tokens", _i32), ("heads_q", _i32), ("heads_k", _i32), ("head_dim", _i32),
+    ]
+
+
 EXPORTED_SYMBOLS = (
     "tilemix_quant_per_block_int8",
     "tilemix_attn_fwd",
     "tilemix_attn_fwd_debug",
+    "tilemix_rms_norm_f16",
+    "tilemix_rotary_f16",
+    "tilemix_silu_mul_f16",
     "tilemix_abi_version",
     "tilemix_params_size",
     "tilemix_last_error",
@@ -119,6 +145,12 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
         lib.tilemix_attn_fwd.restype = ctypes.c_int
         lib.tilemix_attn_fwd_debug.argtypes = [ctypes.POINTER(AttnParams), _vp, _vp, _i64, _i64, _vp]
         lib.tilemix_attn_fwd_debug.restype = ctypes.c_int
+        lib.tilemix_rms_norm_f16.argtypes = [ctypes.POINTER(RmsNormParams), _vp]
+        lib.tilemix_rms_norm_f16.restype = ctypes.c_int
+        lib.tilemix_rotary_f16.argtypes = [ctypes.POINTER(RotaryParams), _vp]
+        lib.tilemix_rotary_f16.restype = ctypes.c_int
+        lib.tilemix_silu_mul_f16.argtypes = [_vp, _vp, _vp, _i64, _vp]
+        lib.tilemix_silu_mul_f16.restype = ctypes.c_int
         lib.tilemix_abi_version.argtypes = []
         lib.tilemix_abi_version.restype = ctypes.c_int
         lib.tilemix_params_size.argtypes = [ctypes.c_int]
@@ -129,7 +161,7 @@ def load_library(path: os.PathLike | str | None = None) -> ctypes.CDLL:
             raise TileMixLibraryError(
                 f"{lib_path}: ABI version {lib.tilemix_abi_version()} != {ABI_VERSION}; rebuild it"
             )
-        for which, struct in ((0, QuantParams), (1, AttnParams)):
+        for which, struct in ((0, QuantParams), (1, AttnParams), (2, RmsNormParams), (3, RotaryParams)):
             if lib.tilemix_params_size(which) != ctypes.sizeof(struct):
                 raise TileMixLibraryError(
                     f"{lib_path}: {struct.__name__} size {lib.tilemix_params_size(which)} != "
@@ -178,3 +210,22 @@ def attn_fwd_debug(params: AttnParams, qk_i32: torch.Tensor | None, qk_f16: torc
             ),
             lib,
         )
+
+
+def rms_norm_f16(params: RmsNormParams, device: torch.device) -> None:
+    lib = load_library()
+    with torch.cuda.device(device):
+        _check(lib.tilemix_rms_norm_f16(ctypes.byref(params), current_stream(device)), lib)
+
+
+def rotary_f16(params: RotaryParams, device: torch.device) -> None:
+    lib = load_library()
+    with torch.cuda.device(device):
+        _check(lib.tilemix_rotary_f16(ctypes.byref(params), current_stream(device)), lib)
+
+
+def silu_mul_f16(gate: torch.Tensor, up: torch.Tensor, out: torch.Tensor) -> None:
+    lib = load_library()
+    device = gate.device
+    with torch.cuda.device(device):
+        _check(lib.tilemix_silu_mul_f16(ptr(gate), ptr(up), ptr(out), gate.numel(), current_stream(device)), lib)

@@ -51,6 +51,26 @@ int tilemix_attn_fwd_debug(const tilemix_attn_params* p, int32_t* qk_i32, void* 
                          static_cast<hipStream_t>(stream));
 }
 
+int tilemix_rms_norm_f16(const tilemix_rmsnorm_params* p, void* stream) {
+  if (p == nullptr) {
+    tmx::set_error("tilemix_rms_norm_f16: null params");
+    return TILEMIX_E_INVALID;
+  }
+  return tmx::launch_rmsnorm(*p, static_cast<hipStream_t>(stream));
+}
+
+int tilemix_rotary_f16(const tilemix_rotary_params* p, void* stream) {
+  if (p == nullptr) {
+    tmx::set_error("tilemix_rotary_f16: null params");
+    return TILEMIX_E_INVALID;
+  }
+  return tmx::launch_rotary(*p, static_cast<hipStream_t>(stream));
+}
+
+int tilemix_silu_mul_f16(const void* gate, const void* up, void* out, int64_t n, void* stream) {
+  return tmx::launch_silu_mul(gate, up, out, n, static_cast<hipStream_t>(stream));
+}
+
 int tilemix_abi_version(void) { return TILEMIX_ABI_VERSION; }
 
 int64_t tilemix_params_size(int which) {
@@ -59,6 +79,10 @@ int64_t tilemix_params_size(int which) {
       return (int64_t)sizeof(tilemix_quant_params);
     case 1:
       return (int64_t)sizeof(tilemix_attn_params);
+    case 2:
+      return (int64_t)sizeof(tilemix_rmsnorm_params);
+    case 3:
+      return (int64_t)sizeof(tilemix_rotary_params);
     default:
       return -1;
   }

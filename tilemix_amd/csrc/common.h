@@ -28,6 +28,9 @@ void set_error(const char* fmt, ...);
 int launch_quant(const tilemix_quant_params& p, hipStream_t stream);
 int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
                 int64_t dump_t, int64_t dump_h, hipStream_t stream);
+int launch_rmsnorm(const tilemix_rmsnorm_params& p, hipStream_t stream);
+int launch_rotary(const tilemix_rotary_params& p, hipStream_t stream);
+int launch_silu_mul(const void* gate, const void* up, void* out, int64_t n, hipStream_t stream);
 
 // Exchange a value between lane l and lane l^32 of a wave64 and combine:
 // returns {value of this lane, value of the partner lane} as (lo, hi) pair

@@ -22,11 +22,12 @@ from torch import Tensor, nn
 from transformers.cache_utils import Cache, DynamicLayer
 from transformers.models.llama.modeling_llama import LlamaAttention, apply_rotary_pos_emb
 
+from .. import _native
 from ..attention.tilemix_varlen import tilemix_varlen_attention
 from ._common import (MIN_TILEMIX_SEQLEN, BucketConfig, TileMixRoutingMixin, pick_block_n_for_64,  # noqa: F401
                       pick_mask_block_n)
 
-__all__ = ["TileMixLlamaAttention", "inject_tilemix_into_llama", "configure_tilemix_attention_pattern",
+__all__ = ["TileMixLlamaAttention", "inject_tilemix_into_llama", "configure_tilemix_attention_pattern", "rms_norm",
            "PrefillCache", "prepare_llama_prefill", "prepare_llama_norms", "rotary_token_major", "silu_mul",
            "PrefillRMSNorm", "PrefillMLP", "build_block_tables", "BucketConfig", "pick_mask_block_n",
            "pick_block_n_for_64"]
@@ -143,8 +144,34 @@ class PrefillCache(Cache):
 
 
 # ---- prefill helpers ---------------------------------------------------------
+def _require_cuda(what: str, *tensors) -> None:
+    if not all(t.is_cuda for t in tensors):
+        raise RuntimeError(f"{what} is a GPU-only HIP kernel (reference: CUDA/Triton only)")
+
+
+def rms_norm(hidden_states, weight, eps: float):
+    """HIP RMSNorm over the last dim: weight * fp16(x * rsqrt(mean(x^2) + eps)),
+    the mean in fp32 (reference models/tilemix_llama.py:718-797)."""
+    if hidden_states.dtype != torch.float16 or weight.dtype != torch.float16:
+        raise ValueError("prefill RMSNorm requires FP16 operands")
+    cols = hidden_states.shape[-1]
+    if weight.shape != (cols,) or not weight.is_contiguous():
+        raise ValueError("RMSNorm weight must be a contiguous vector over the last dim")
+    _require_cuda("prefill RMSNorm", hidden_states, weight)
+    x = hidden_states if hidden_states.stride(-1) == 1 else hidden_states.contiguous()
+    x2 = x.reshape(-1, cols)  # a view whenever rows are uniformly strided
+    out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    p = _native.RmsNormParams()
+    p.x, p.weight, p.out = x2.data_ptr(), weight.data_ptr(), out.data_ptr()
+    p.rows, p.stride_x, p.stride_out = x2.shape[0], x2.stride(0) if x2.shape[0] > 1 else cols, cols
+    p.cols, p.eps = cols, float(eps)
+    _native.rms_norm_f16(p, x.device)
+    return out
+
+
 class PrefillRMSNorm(nn.Module):
-    """weight * fp16(x * rsqrt(mean(x^2) + eps)), the mean in fp32 (reference :776-787)."""
+    """weight * fp16(x * rsqrt(mean(x^2) + eps)), the mean in fp32 (reference :776-797),
+    one HIP kernel."""
 
     def __init__(self, original):
         super().__init__()
@@ -153,9 +180,7 @@ class PrefillRMSNorm(nn.Module):
         self.train(original.training)
 
     def forward(self, hidden_states):
-        x = hidden_states.float()
-        var = x.square().mean(dim=-1, keepdim=True)
-        return self.weight * (x * torch.rsqrt(var + self.variance_epsilon)).to(hidden_states.dtype)
+        return rms_norm(hidden_states, self.weight, self.variance_epsilon)
 
 
 def prepare_llama_norms(model):
@@ -167,8 +192,9 @@ def prepare_llama_norms(model):
 
 def rotary_token_major(q, k, cos, sin):
     """Split-half RoPE whose outputs are token-major ``[b, t, h, d]`` tensors
-    returned as ``[b, h, t, d]`` views (reference :827-846): q*cos and
-    rotate(q)*sin are each rounded to fp16 and their sum is rounded to fp16."""
+    returned as ``[b, h, t, d]`` views (reference :808-847): q*cos and
+    rotate(q)*sin are each rounded to fp16 and their sum is rounded to fp16.
+    One HIP kernel for Q and K."""
     b, hq, t, d = q.shape
     hk = k.shape[1]
     if q.dtype != torch.float16 or any(x.dtype != q.dtype for x in (k, cos, sin)):
@@ -179,30 +205,33 @@ def rotary_token_major(q, k, cos, sin):
         raise ValueError("rotary batch must be one or match the input")
     if q.stride(-1) != 1 or k.stride(-1) != 1 or cos.stride(-1) != 1 or sin.stride(-1) != 1:
         raise ValueError("rotary operands must have contiguous head dimensions")
-    c = cos[:, None].float()
-    s = sin[:, None].float()
-
-    def rope(x, heads):
-        xf = x.float()
-        half = d // 2
-        rot = torch.cat((-xf[..., half:], xf[..., :half]), dim=-1)
-        y = (xf * c).half().float() + (rot * s).half().float()
-        out = torch.empty((b, t, heads, d), device=x.device, dtype=x.dtype)
-        out.copy_(y.transpose(1, 2))
-        return out.transpose(1, 2)
-
-    return rope(q, hq), rope(k, hk)
+    _require_cuda("prefill rotary", q, k, cos, sin)
+    oq = torch.empty((b, t, hq, d), device=q.device, dtype=q.dtype)
+    ok = torch.empty((b, t, hk, d), device=k.device, dtype=k.dtype)
+    p = _native.RotaryParams()
+    p.q, p.k, p.cos, p.sin = q.data_ptr(), k.data_ptr(), cos.data_ptr(), sin.data_ptr()
+    p.q_out, p.k_out = oq.data_ptr(), ok.data_ptr()
+    p.stride_q_batch, p.stride_q_head, p.stride_q_token = q.stride(0), q.stride(1), q.stride(2)
+    p.stride_k_batch, p.stride_k_head, p.stride_k_token = k.stride(0), k.stride(1), k.stride(2)
+    p.stride_cos_batch = cos.stride(0) if cos.shape[0] > 1 else 0
+    p.stride_cos_token = cos.stride(1)
+    p.stride_sin_batch = sin.stride(0) if sin.shape[0] > 1 else 0
+    p.stride_sin_token = sin.stride(1)
+    p.batch, p.tokens, p.heads_q, p.heads_k, p.head_dim = b, t, hq, hk, d
+    _native.rotary_f16(p, q.device)
+    return oq.transpose(1, 2), ok.transpose(1, 2)
 
 
 def silu_mul(gate, up):
-    """fp16(silu(gate)) * up in fp32, rounded to fp16 (reference :849-868)."""
+    """fp16(silu(gate)) * up in fp32, rounded to fp16 (reference :849-868), one HIP kernel."""
     if gate.dtype != torch.float16 or up.dtype != gate.dtype or gate.shape != up.shape:
         raise ValueError("SiLU requires equally shaped FP16 operands")
     if not gate.is_contiguous() or not up.is_contiguous():
         raise ValueError("SiLU requires contiguous operands")
-    g = gate.float()
-    act = (g / (1.0 + torch.exp(-g))).half()
-    return (act.float() * up.float()).half()
+    _require_cuda("prefill SiLU", gate, up)
+    out = torch.empty_like(gate)
+    _native.silu_mul_f16(gate, up, out)
+    return out
 
 
 class PrefillMLP(nn.Module):
