@@ -262,6 +262,12 @@ def main() -> int:
 
     kernel_fn(bm50)()
     if args.kernel_only:
+        # Bring the GPU to its steady clocks first (~0.3 s of fp16 GEMMs, a
+        # different kernel, so the profiled attention launches are all warm).
+        a = torch.randn(8192, 8192, device=device, dtype=torch.float16)
+        for _ in range(600):
+            a @ a
+        torch.cuda.synchronize()
         for _ in range(args.kernel_only):
             kernel_fn(bm50)()
         torch.cuda.synchronize()
