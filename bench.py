@@ -21,6 +21,7 @@ init fp16 Llama-3.2-3B prefill, B=8 x 4096, TileMix SpTrans50 in every layer).
 from __future__ import annotations
 
 import argparse
+import itertools
 import json
 import os
 import platform
@@ -163,6 +164,67 @@ def e2e_prefill(device, runs: int = 20, warmup: int = 5, seed: int = 0):
     del model
     torch.cuda.empty_cache()
     return statistics.median(times), times
+
+
+def other_configs(device, steps: int):
+    """BASELINE configs 3 and 4 (parity-test shapes, reported for information):
+    one tilemix_attention_with_quant step each, effective TOPS and the blended
+    roofline fraction of the step.  cfg3: Qwen2-7B shape, B1 x 32768, Hq28/Hk4,
+    D128, row_rand and bigbird at p = 0.5 (mask groups of 8 tiles).  cfg4: 24
+    packed sequences of 512..8192 tokens, Hq32/Hk8, align_sparse at p = 0.5."""
+    import torch
+    from tilemix_amd.attention import precision_maps as pm
+    from tilemix_amd.attention.hip import tilemix as tmx
+    from tilemix_amd.models._common import pick_mask_block_n
+
+    def run(lengths, hq, hk, pattern, bnm, seed, head_scale):
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        n = sum(lengths)
+        q = torch.randn((n, hq, D), generator=g, device=device)
+        k = torch.randn((n, hk, D), generator=g, device=device)
+        v = torch.randn((n, hk, D), generator=g, device=device)
+        if head_scale:
+            q *= torch.rand((1, hq, 1), generator=g, device=device) * 1.5 + 0.5
+            k *= torch.rand((1, hk, 1), generator=g, device=device) * 1.5 + 0.5
+            v *= torch.rand((1, hk, 1), generator=g, device=device) * 1.5 + 0.5
+        q, k, v = q.half(), k.half(), v.half()
+        cu = torch.tensor([0] + list(itertools.accumulate(lengths)), dtype=torch.int32, device=device)
+        lmax = max(lengths)
+        row = pm.make_precision_bitmask(lmax, 128, bnm, None, percentage=0.5, pattern_type=pattern,
+                                        pattern_params={}, COMPUTE_BLOCK_N=64)
+        bm = row.repeat(hk).to(device)
+        fn = lambda: tmx.tilemix_attention_with_quant(q, k, v, cu, cu, lmax, lmax, bm, block_m=128, block_n=64,
+                                                      block_n_mask=bnm, BLKQ=128, BLKK=64, causal=True,
+                                                      int8_use_fp16_v=True)
+        ms = time_steps(fn, steps, 3)
+        ops = sum(algorithmic_ops(1, hq, D, ln) for ln in lengths)
+        # INT8 fraction of the executed tiles, per sequence (row = hk * m_blocks(seq) + m)
+        bits = [int(x) for x in row.tolist()] * hk
+        total = routed = 0.0
+        for ln in lengths:
+            mbz = (ln + 127) // 128
+            nt = (ln + 63) // 64
+            for h in range(hk):
+                for m in range(mbz):
+                    raw = bits[h * mbz + m]
+                    for t in range(min(nt, ((m + 1) * 128 + 63) // 64)):
+                        total += 1
+                        routed += (raw >> (t // (bnm // 64))) & 1
+        f = routed / total
+        del q, k, v
+        torch.cuda.empty_cache()
+        return {"step_ms": ms, "eff_tops": ops / (ms * 1e-3) / 1e12, "int8_fraction": f,
+                "roofline_frac": roofline_seconds(f, ops) / (ms * 1e-3)}
+
+    out = {}
+    for pattern in ("row_rand", "bigbird"):
+        out[f"cfg3_{pattern}50"] = run([32768], 28, 4, pattern, 512, 3, True)
+    rng = torch.Generator().manual_seed(4)
+    lengths = [int(x) for x in torch.randint(512, 8193, (24,), generator=rng)]
+    out["cfg4_align_sparse50"] = run(lengths, 32, 8, "align_sparse", pick_mask_block_n(max(lengths), 64), 5, False)
+    out["cfg4_align_sparse50"]["tokens"] = sum(lengths)
+    return out
 
 
 def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 1):
@@ -309,6 +371,10 @@ def main() -> int:
             sweep[str(p)] = {"int8_fraction": fp, "step_ms": sp, "kernel_ms": kp,
                              "kernel_roofline_frac": roofline_seconds(fp, ops) / (kp * 1e-3)}
 
+    others = None
+    if args.sweep:
+        others = other_configs(device, args.steps)
+
     e2e_ms = None
     if not args.no_e2e:
         e2e_ms, _ = e2e_prefill(device)
@@ -360,6 +426,7 @@ def main() -> int:
             "quant_plus_launch_ms": ms - k_ms,
             "step_ms_q_prepass": ms_prepass,
             "sweep": sweep,
+            "other_configs": others,
             "e2e_prefill_ms": e2e_ms,
             "e2e_note": "median of 20 after 5 warmups, random-init fp16 Llama-3.2-3B, B8 x 4096, SpTrans50, logits_to_keep=1",
         },

@@ -181,7 +181,7 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.q_fused = (need_int8 && p.q_quant_in_kernel) ? 1 : 0;
   const bool dump = dump_i32 != nullptr || dump_f16 != nullptr;
   a.total_items = (int)total;
-  a.per_xcd = (int)((total + 7) / 8);
+  a.per_xcd = (int)work_items_per_xcd((int64_t)p.heads_k * p.batch, (int64_t)m_blocks * a.group);
 
   const int dp = p.head_dim <= 64 ? 64 : 128;
   dispatch_attn(a, p.block_m, dp, p.routing_mode, int8v, dump, p.bias != nullptr, stream);

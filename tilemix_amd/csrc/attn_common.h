@@ -45,6 +45,29 @@ struct AttnKArgs {
   int per_xcd;
 };
 
+// Work item of workgroup `bid`, or -1.  Items are numbered
+// ((z * hk + kv_head) * m_blocks + mrev) * group + g, so one (sequence, kv head)
+// "group" is ipg = m_blocks * group consecutive items.  Workgroups reach the 8
+// XCDs round-robin (bid & 7); the j-th workgroup of XCD x takes
+//   * while whole rounds of 8 groups remain: group x + 8 (j / ipg), item
+//     j % ipg -- a group stays on one XCD (its L2 serves every re-read of the
+//     group's K/V tiles) and groups are dealt round-robin, so every XCD gets
+//     the same mix of long and short sequences;
+//   * for the last G % 8 groups: their items dealt over all 8 XCDs (item
+//     8 j' + x), which also covers a launch with fewer than 8 groups.
+// per_xcd (the grid is 8 * per_xcd) = (G / 8) * ipg + ceil((G % 8) * ipg / 8).
+__host__ __device__ inline int64_t work_items_per_xcd(int64_t groups, int64_t ipg) {
+  return (groups / 8) * ipg + ((groups % 8) * ipg + 7) / 8;
+}
+__device__ __forceinline__ int work_item(int bid, int total_items, int ipg) {
+  const int x = bid & 7, j = bid >> 3;
+  const int groups = total_items / ipg;
+  const int full_j = (groups / 8) * ipg;  // workgroups per XCD in whole rounds
+  if (j < full_j) return (x + 8 * (j / ipg)) * ipg + j % ipg;
+  const int item = (groups / 8) * 8 * ipg + 8 * (j - full_j) + x;
+  return item < total_items ? item : -1;
+}
+
 typedef __attribute__((address_space(3))) void lds_void;
 typedef short s16x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));

@@ -28,11 +28,11 @@
 //     pattern of the MFMA operands bank-conflict free;
 //   * INT8 tiles accumulate on top of a magic bias (1.5*2^23 as int bits) so
 //     the exact fp32(acc)*ss of the reference is one FMA;
-//   * blockIdx -> work mapping is XCD-aware: each of the 8 XCDs receives a
-//     contiguous range of (sequence, kv-head) groups, so the query heads that
-//     share K/V (GQA) and all query blocks of a head hit the same L2; within a
+//   * blockIdx -> work mapping is XCD-aware (work_item in attn_common.h):
+//     whole (sequence, kv-head) groups are dealt round-robin to the 8 XCDs, so
+//     the query heads that share K/V (GQA) and all query blocks of a head hit
+//     the same L2 and every XCD gets the same mix of sequence lengths; within a
 //     group, query blocks are issued longest-first (causal).
-#pragma once
 #pragma once
 
 #include "attn_common.h"
@@ -68,8 +68,8 @@ attn32_kernel(const AttnKArgs a) {
 
   // ---- work item ---------------------------------------------------------
   const int bid = blockIdx.x;
-  const int lam = (bid & 7) * a.per_xcd + (bid >> 3);
-  if (lam >= a.total_items) return;
+  const int lam = work_item(bid, a.total_items, a.m_blocks * a.group);
+  if (lam < 0) return;
   int t = lam;
   const int g = t % a.group;
   t /= a.group;
