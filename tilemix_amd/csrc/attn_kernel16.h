@@ -145,13 +145,14 @@ attn16_kernel(const AttnKArgs a) {
     if (MODE == TILEMIX_ROUTING_INT8) return 1;
     return (int)((bits >> (unsigned)(n / a.mask_tiles)) & 1ull);
   };
-  // K scale of tile n (reference :380-388: clamped block index), fp16.
-  auto load_sk = [&](int n) -> f16 {
+  // K (and int8 V) scale of tile n (reference :380-388: clamped block
+  // index), fp16, fetched with the tile's copy.
+  auto load_scale = [&](const f16* sc, const int32_t* cus, int n) -> f16 {
     f16 s = (f16)1.0f;
-    const int kbase = a.cu_ks[z], kend = a.cu_ks[z + 1];
-    if (kend > kbase) {
-      const int idx = min(kbase + (n * kBN) / a.blkk, kend - 1);
-      s = a.sk[(int64_t)idx * a.hk + hk];
+    const int base = cus[z], end = cus[z + 1];
+    if (end > base) {
+      const int idx = min(base + (n * kBN) / a.blkk, end - 1);
+      s = sc[(int64_t)idx * a.hk + hk];
     }
     return s;
   };
@@ -178,38 +179,41 @@ attn16_kernel(const AttnKArgs a) {
     else sw = rowb == 256 ? swz_k<256>(r) : rowb == 128 ? swz_k<128>(r) : swz_k<64>(r);
     return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
   };
-  auto issue_tile = [&](int n, int route, unsigned char* stage) {
+  // Copies are issued from inline assembly (async_load16_asm): the loop
+  // orders them against its LDS reads itself (s_waitcnt + barrier per tile).
+  const uint32_t smem_lds = lds_addr(smem);
+  auto issue_tile = [&](int n, int route, uint32_t stage) {
     const int key0 = n * kBN;
     const int rem = Lk - key0;  // >= 1
     if (route == 0) {
-      const auto rs = make_rsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
+      const SRsrc rs = make_srsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
 #pragma unroll
       for (int i = 0; i < K16_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K16_T) async_load16(rs, lane_off(L, ROW16, kt_bytes, 0), stage + L * 1024);
+        if (L < K16_T) async_load16_asm(rs, lane_off(L, ROW16, kt_bytes, 0), stage + L * 1024);
       }
     } else {
-      const auto rs = make_rsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
+      const SRsrc rs = make_srsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
 #pragma unroll
       for (int i = 0; i < K8_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K8_T) async_load16(rs, lane_off(L, ROW8, k8t_bytes, 0), stage + L * 1024);
+        if (L < K8_T) async_load16_asm(rs, lane_off(L, ROW8, k8t_bytes, 0), stage + L * 1024);
       }
     }
-    unsigned char* vstage = stage + KBUF;
+    const uint32_t vstage = stage + KBUF;
     if (!INT8V || route == 0) {
-      const auto rs = make_rsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
+      const SRsrc rs = make_srsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
 #pragma unroll
       for (int i = 0; i < K16_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K16_T) async_load16(rs, lane_off(L, ROW16, vt_bytes, 1), vstage + L * 1024);
+        if (L < K16_T) async_load16_asm(rs, lane_off(L, ROW16, vt_bytes, 1), vstage + L * 1024);
       }
     } else {
-      const auto rs = make_rsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
+      const SRsrc rs = make_srsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
 #pragma unroll
       for (int i = 0; i < K8_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K8_T) async_load16(rs, lane_off(L, ROW8, v8t_bytes, 2), vstage + L * 1024);
+        if (L < K8_T) async_load16_asm(rs, lane_off(L, ROW8, v8t_bytes, 2), vstage + L * 1024);
       }
     }
   };
@@ -226,16 +230,23 @@ attn16_kernel(const AttnKArgs a) {
   for (int db = 0; db < NDB; ++db) acc[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   int route_next = 0;
-  f16 sk_next = (f16)1.0f;
+  f16 sk_next = (f16)1.0f, sv_next = (f16)1.0f;
+  auto fetch_scales = [&](int n) {
+    if (MODE != TILEMIX_ROUTING_FP16 && route_next == 1) {
+      sk_next = load_scale(a.sk, a.cu_ks, n);
+      if (INT8V) sv_next = load_scale(a.sv, a.cu_vs, n);
+    }
+  };
   if (n_blocks > 0) {
     route_next = route_of(0);
-    if (MODE != TILEMIX_ROUTING_FP16 && route_next == 1) sk_next = load_sk(0);
-    issue_tile(0, route_next, smem);
+    fetch_scales(0);
+    issue_tile(0, route_next, smem_lds);
   }
 
   for (int n = 0; n < n_blocks; ++n) {
     const int route = route_next;
     const f16 sk16 = sk_next;
+    const f16 sv16 = sv_next;
     unsigned char* stage = smem + (n & 1) * STAGE;
     // Tile n has landed (own loads), then every wave's loads have landed and
     // every wave is done with the other stage (tile n-1).
@@ -243,8 +254,8 @@ attn16_kernel(const AttnKArgs a) {
     __syncthreads();
     if (n + 1 < n_blocks) {
       route_next = route_of(n + 1);
-      if (MODE != TILEMIX_ROUTING_FP16 && route_next == 1) sk_next = load_sk(n + 1);
-      issue_tile(n + 1, route_next, smem + ((n + 1) & 1) * STAGE);
+      fetch_scales(n + 1);
+      issue_tile(n + 1, route_next, smem_lds + ((n + 1) & 1) * STAGE);
     }
 
     const int key0 = n * kBN;
@@ -401,12 +412,6 @@ attn16_kernel(const AttnKArgs a) {
     if (INT8V && route == 1) {
       // Reference :449-497: PV on int8 V codes with p scaled by the V block
       // scale in fp16: p_scaled = fp16(p * sv) (l keeps the unscaled p).
-      f16 sv16 = (f16)1.0f;
-      const int vb = a.cu_vs[z], ve = a.cu_vs[z + 1];
-      if (ve > vb) {
-        const int idx = min(vb + key0 / a.blkk, ve - 1);
-        sv16 = a.sv[(int64_t)idx * a.hk + hk];
-      }
       const f16x2 sv2 = {sv16, sv16};
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb)
