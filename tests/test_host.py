@@ -55,12 +55,16 @@ def test_abi_version_and_struct_layout(lib):
     assert lib.tilemix_abi_version() == abi == _native.ABI_VERSION
     assert lib.tilemix_params_size(0) == ctypes.sizeof(_native.QuantParams)
     assert lib.tilemix_params_size(1) == ctypes.sizeof(_native.AttnParams)
+    assert lib.tilemix_params_size(2) == ctypes.sizeof(_native.RmsNormParams)
+    assert lib.tilemix_params_size(3) == ctypes.sizeof(_native.RotaryParams)
     assert lib.tilemix_params_size(7) == -1
 
 
 def test_ctypes_mirror_matches_header_field_order():
     text = HEADER.read_text()
-    for struct, cls in (("tilemix_quant_params", _native.QuantParams), ("tilemix_attn_params", _native.AttnParams)):
+    for struct, cls in (("tilemix_quant_params", _native.QuantParams), ("tilemix_attn_params", _native.AttnParams),
+                        ("tilemix_rmsnorm_params", _native.RmsNormParams),
+                        ("tilemix_rotary_params", _native.RotaryParams)):
         body = re.search(r"typedef struct %s \{(.*?)\} %s;" % (struct, struct), text, re.S).group(1)
         body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
         fields = []
@@ -121,6 +125,32 @@ def test_quant_validation_messages(lib):
     p.heads, p.batch, p.blk_tokens, p.head_dim = 2, 1, 64, 12
     assert lib.tilemix_quant_per_block_int8(ctypes.byref(p), None) == 1
     assert b"head_dim" in lib.tilemix_last_error()
+
+
+def test_prefill_helper_validation_messages(lib):
+    assert lib.tilemix_rms_norm_f16(None, None) == 1
+    assert b"null params" in lib.tilemix_last_error()
+    assert lib.tilemix_rotary_f16(None, None) == 1
+    assert b"null params" in lib.tilemix_last_error()
+    assert lib.tilemix_silu_mul_f16(None, None, None, 4, None) == 1
+    assert b"null tensor pointer" in lib.tilemix_last_error()
+    dummy = ctypes.c_void_p(16)  # never dereferenced: validation fails first
+    assert lib.tilemix_silu_mul_f16(dummy, dummy, dummy, -1, None) == 1
+    assert lib.tilemix_silu_mul_f16(dummy, dummy, dummy, 0, None) == 0  # nothing to do
+    p = _native.RmsNormParams()
+    assert lib.tilemix_rms_norm_f16(ctypes.byref(p), None) == 1
+    assert b"null tensor pointer" in lib.tilemix_last_error()
+    p.x = p.weight = p.out = dummy
+    p.rows, p.cols, p.stride_x, p.stride_out, p.eps = 4, 64, 32, 64, 1e-6
+    assert lib.tilemix_rms_norm_f16(ctypes.byref(p), None) == 1
+    assert b"invalid shape" in lib.tilemix_last_error()
+    r = _native.RotaryParams()
+    assert lib.tilemix_rotary_f16(ctypes.byref(r), None) == 1
+    assert b"null tensor pointer" in lib.tilemix_last_error()
+    r.q = r.k = r.cos = r.sin = r.q_out = r.k_out = dummy
+    r.batch, r.tokens, r.heads_q, r.heads_k, r.head_dim = 1, 8, 2, 1, 15
+    assert lib.tilemix_rotary_f16(ctypes.byref(r), None) == 1
+    assert b"invalid shape" in lib.tilemix_last_error()
 
 
 # ------------------------------------------------------- host-side logic
