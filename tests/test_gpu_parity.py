@@ -296,3 +296,31 @@ def test_in_kernel_q_quant_bitexact(device, case, monkeypatch):
     out_fus, _ = tmx.tilemix_attention_with_quant(*args, **ekw)
     torch.cuda.synchronize()
     assert torch.equal(out_pre, out_fus)
+
+
+@pytest.mark.parametrize("block_m", [64, 128])
+def test_queries_shorter_than_keys(device, block_m):
+    """Separate cu_seqlens for Q and K (a query suffix over a longer key
+    prefix): the causal limit of row r is key r + Lk - Lq (reference :256-262)."""
+    pairs = [(100, 300), (300, 300), (1, 64), (200, 257)]
+    hq, hk, d = 4, 2, 128
+    rng = np.random.default_rng(41)
+    lq = [p[0] for p in pairs]
+    lk = [p[1] for p in pairs]
+    q = rng.standard_normal((sum(lq), hq, d), dtype=np.float32).astype(np.float16)
+    k = rng.standard_normal((sum(lk), hk, d), dtype=np.float32).astype(np.float16)
+    v = rng.standard_normal((sum(lk), hk, d), dtype=np.float32).astype(np.float16)
+    cuq = np.concatenate([[0], np.cumsum(lq)]).astype(np.int32)
+    cuk = np.concatenate([[0], np.cumsum(lk)]).astype(np.int32)
+    mx = max(max(lq), max(lk))
+    bits = random_bitmask(hk, -(-mx // block_m), seed=41)
+    out, _ = tmx.tilemix_attention_with_quant(
+        to_dev(q, device), to_dev(k, device), to_dev(v, device), to_dev(cuq, device), to_dev(cuk, device),
+        mx, mx, bitmask_tensor(bits, device), block_m=block_m, block_n=64, block_n_mask=64, BLKQ=128, BLKK=64,
+        causal=True, routing_mode="mixed", scalar_scales=(block_m == 128), int8_use_fp16_v=True)
+    q8, sq, cq = O.quant_per_block_int8(q, cuq, 128)
+    k8, sk, ck = O.quant_per_block_int8(k, cuk, 64)
+    ref = O.attn_fwd(q, k, v, cuq, cuk, bits, block_m=block_m, block_n_mask=64, causal=True,
+                     q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
+                     cu_q_scale=cq, cu_k_scale=ck)
+    assert_close_out(out.cpu().numpy(), ref)
