@@ -132,24 +132,15 @@ __device__ __forceinline__ float2 pair32(float x) {
   return make_float2(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Raw buffer over [base, base + bytes): loads at offsets >= bytes return 0.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
-}
-
-// 16 bytes per lane from the buffer straight into LDS: lane l writes
-// lds_wave_base + 16 l (buffer_load_dwordx4 ... lds).
-__device__ __forceinline__ void async_load16(__amdgpu_buffer_rsrc_t rsrc, int voffset, unsigned char* lds_wave_base) {
-  __builtin_amdgcn_raw_ptr_buffer_load_lds(rsrc, (lds_void*)lds_wave_base, 16, voffset, 0, 0, 0);
-}
-
-// The same HBM -> LDS copy issued from inline assembly, for kernels that
-// order it against their LDS reads themselves (s_waitcnt vmcnt(0) + barrier
-// before a stage is read).  Issued through the builtin, the compiler cannot
-// tell the stage being filled from the stage being read and waits for the
-// copy before every LDS read, which serialises the prefetch with the tile's
-// compute.  rsrc and lds_addr are wave-uniform (SGPRs); M0 carries the LDS
-// address, and one wait state separates its write from the load.
+// HBM -> LDS copy of 16 bytes per lane (buffer_load_dwordx4 ... lds: lane l
+// writes lds + 16 l) through a raw buffer over [base, base + bytes), so loads
+// at offsets >= bytes return 0.  Issued from inline assembly: the kernels
+// order the copies against their LDS reads themselves (s_waitcnt vmcnt(0) +
+// barrier before a stage is read).  Through the compiler builtin, the
+// compiler cannot tell the stage being filled from the stage being read and
+// waits for the copy before every LDS read, which serialises the prefetch with
+// the tile's compute.  rsrc and lds are wave-uniform (SGPRs); M0 carries the
+// LDS address, and one wait state separates its write from the load.
 struct SRsrc {
   i32x4 w;
 };
