@@ -227,7 +227,7 @@ def other_configs(device, steps: int):
     return out
 
 
-def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 1):
+def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 4):
     """Oracle (numpy fp32 emulation) on sequence 0, the first `sample_groups`
     KV groups (3 query heads each), quantisation included; scaled to TOPS."""
     import numpy as np
@@ -254,7 +254,7 @@ def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 1):
         "cores": int(threads),
         "kind": "port",
         "sample": (f"numpy oracle (fp32 emulation incl. int8 quantisation), sequence 0, "
-                   f"{hq} query heads / {sample_groups} KV head of the B8 L4096 SpTrans50 workload; "
+                   f"{hq} query heads / {sample_groups} KV heads of the B8 L4096 SpTrans50 workload; "
                    f"{secs:.2f} s for {ops:.3e} ops; host {platform.processor() or platform.machine()}, "
                    f"os.cpu_count()={os.cpu_count()}"),
         "seconds": secs,
