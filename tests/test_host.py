@@ -114,6 +114,16 @@ def test_attn_validation_messages(lib):
     p.precision_bitmask = dummy
     assert lib.tilemix_attn_fwd(ctypes.byref(p), None) == 1
     assert b"int8 routing needs" in lib.tilemix_last_error()
+    # A short sequence with a huge token stride: the lane offsets of one
+    # 64-key tile (not just max_seqlen_k rows) must fit the 32-bit buffer range.
+    p.routing_mode = 1
+    p.max_seqlen_q = p.max_seqlen_k = 4
+    aligned_dummy = ctypes.c_void_p(1 << 12)
+    for f in ("q", "k", "v", "out"):
+        setattr(p, f, aligned_dummy)
+    p.stride_k_token = p.stride_v_token = 1 << 25  # 64 MiB per token
+    assert lib.tilemix_attn_fwd(ctypes.byref(p), None) == 1
+    assert b"exceeds 2 GiB" in lib.tilemix_last_error()
 
 
 def test_quant_validation_messages(lib):

@@ -112,8 +112,9 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
     return TILEMIX_E_INVALID;
   }
 
-  // K/V tiles are read through 32-bit raw buffers spanning one sequence.
-  const int64_t span = (int64_t)p.max_seqlen_k *
+  // K/V tiles are read through 32-bit raw buffers spanning one sequence; the
+  // per-lane offsets of a tile reach 64 rows even when the sequence is shorter.
+  const int64_t span = (int64_t)std::max(p.max_seqlen_k, 64) *
                        (int64_t)std::max(std::max(p.stride_k_token, p.stride_v_token) * 2,
                                          std::max(p.stride_k8_token, p.stride_v8_token));
   if (span >= ((int64_t)1 << 31)) {

@@ -194,7 +194,10 @@ attn32_kernel(const AttnKArgs a) {
   // Each tile is fetched through raw buffers based at the tile's first key
   // and sized to the keys left in the sequence: rows past the end read as 0
   // (finite bytes for masked keys, which contribute exactly 0 through p = 0).
-  // Per-lane offsets are loop-invariant; the per-tile work is scalar.
+  // Per-lane offsets are loop-invariant; the per-tile work is scalar.  The
+  // swizzle of a copied row depends only on its index mod 16, and the rows of
+  // copy i are those of copy 0 plus i * NW * rows-per-copy (a multiple of 16),
+  // so one lane offset per stream serves every copy of a tile.
   const int64_t kt_bytes = a.sk_t * 2, vt_bytes = a.sv_t * 2;
   const int64_t k8t_bytes = a.sk8_t, v8t_bytes = a.sv8_t;
   const unsigned char* kseq = reinterpret_cast<const unsigned char*>(a.k + (int64_t)k_start * a.sk_t + (int64_t)hk * a.sk_h);
@@ -203,41 +206,57 @@ attn32_kernel(const AttnKArgs a) {
       ? reinterpret_cast<const unsigned char*>(a.k8 + (int64_t)k_start * a.sk8_t + (int64_t)hk * a.sk8_h) : nullptr;
   const unsigned char* v8seq = INT8V
       ? reinterpret_cast<const unsigned char*>(a.v8 + (int64_t)k_start * a.sv8_t + (int64_t)hk * a.sv8_h) : nullptr;
-  auto lane_off = [&](int i, int rowb, int64_t tok_bytes, bool vswz) -> int {
+  auto lane_off0 = [&](int rowb, int64_t tok_bytes, bool vswz) -> int {
     const int rpi = 1024 / rowb, cpr = rowb / 16;
-    const int r = (i * NW + wave) * rpi + lane / cpr;
+    const int r = wave * rpi + lane / cpr;
     int sw;
     if (rowb == 256) sw = vswz ? swz_v32<256>(r) : swz_k<256>(r);
     else if (rowb == 128) sw = vswz ? swz_v32<128>(r) : swz_k<128>(r);
     else sw = swz_k<64>(r);
     return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
   };
+  const int dma_k16 = lane_off0(ROW16, kt_bytes, false);
+  const int dma_k8 = MODE != TILEMIX_ROUTING_FP16 ? lane_off0(ROW8, k8t_bytes, false) : 0;
+  const int dma_v16 = lane_off0(ROW16, vt_bytes, true);
+  const int dma_v8 = INT8V ? lane_off0(ROW8, v8t_bytes, false) : 0;
+  const int step_k16 = NW * (1024 / ROW16) * (int)kt_bytes;
+  const int step_k8 = NW * (1024 / ROW8) * (int)k8t_bytes;
+  const int step_v16 = NW * (1024 / ROW16) * (int)vt_bytes;
+  const int step_v8 = NW * (1024 / ROW8) * (int)v8t_bytes;
   const uint32_t smem_lds = lds_addr(smem);
   auto issue_tile = [&](int n, int route, uint32_t stage) {
     const int key0 = n * kBN;
     const int rem = Lk - key0;  // >= 1
     if (route == 0) {
       const SRsrc rs = make_srsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
+      int o = dma_k16;
+      asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < K16_INS; ++i)
-        async_load16_asm(rs, lane_off(i, ROW16, kt_bytes, false), stage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, o + i * step_k16, stage + (i * NW + wave) * 1024);
     } else {
       const SRsrc rs = make_srsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
+      int o = dma_k8;
+      asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < K8_INS; ++i)
-        async_load16_asm(rs, lane_off(i, ROW8, k8t_bytes, false), stage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, o + i * step_k8, stage + (i * NW + wave) * 1024);
     }
     const uint32_t vstage = stage + KBUF;
     if (!INT8V || route == 0) {
       const SRsrc rs = make_srsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
+      int o = dma_v16;
+      asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < V16_INS; ++i)
-        async_load16_asm(rs, lane_off(i, ROW16, vt_bytes, true), vstage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, o + i * step_v16, vstage + (i * NW + wave) * 1024);
     } else {
       const SRsrc rs = make_srsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
+      int o = dma_v8;
+      asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < V8_INS; ++i)
-        async_load16_asm(rs, lane_off(i, ROW8, v8t_bytes, false), vstage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, o + i * step_v8, vstage + (i * NW + wave) * 1024);
     }
   };
 
@@ -293,12 +312,16 @@ attn32_kernel(const AttnKArgs a) {
 
   // The magic bias as the MFMA C operand of the first k-step of every INT8
   // tile, kept in VGPRs for the whole loop (the barrier stops the compiler from
-  // rebuilding the 16 constants before every INT8 tile).
+  // rebuilding the 16 constants before every INT8 tile).  The int8-V variant
+  // needs those 16 VGPRs for its V path: it accumulates from zero and adds the
+  // bias bits to the int32 result instead (the same float bits).
+  constexpr bool kMagicC = !INT8V;
+  constexpr int kBiasAdd = kMagicC ? 0 : 0x4B400000;
   i32x16 magic_c;
 #pragma unroll
   for (int e = 0; e < 16; ++e) {
     int mv = 0x4B400000;
-    if (MODE != TILEMIX_ROUTING_FP16) asm volatile("" : "+v"(mv));
+    if (MODE != TILEMIX_ROUTING_FP16 && kMagicC) asm volatile("" : "+v"(mv));
     magic_c[e] = mv;
   }
   int route_next = 0;
@@ -326,14 +349,14 @@ attn32_kernel(const AttnKArgs a) {
     // ---- S^T = K . Q^T, rounded to fp16 (packed pairs r, r+1) ----------
     uint32_t s16[2][8];
     if (route == 0) {
+      int kbase16 = l32 * ROW16 + ((16 * hi) ^ (16 * swz_k<ROW16>(l32)));
+      asm volatile("" : "+v"(kbase16));
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         f32x16 c = {};
-        const int r = kb * 32 + l32;
 #pragma unroll
         for (int ks = 0; ks < KS16; ++ks) {
-          const int ch = (2 * ks + hi) ^ swz_k<ROW16>(r);
-          const f16x8 av = *reinterpret_cast<const f16x8*>(stage + r * ROW16 + ch * 16);
+          const f16x8 av = *reinterpret_cast<const f16x8*>(stage + (kbase16 ^ (32 * ks)) + kb * 32 * ROW16);
           c = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, qf[ks], c, 0, 0, 0);
         }
         if (DUMP && a.dump_i32 != nullptr && row_ok) {
@@ -360,15 +383,15 @@ attn32_kernel(const AttnKArgs a) {
       // exact: ss has 11 significant bits).
       constexpr float kMagic = 12582912.0f;
       const float negms = -kMagic * ss;
+      int kbase8 = l32 * ROW8 + ((16 * hi) ^ (16 * swz_k<ROW8>(l32)));
+      asm volatile("" : "+v"(kbase8));
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
         i32x16 c;
-        const int r = kb * 32 + l32;
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) {
-          const int ch = (2 * ks + hi) ^ swz_k<ROW8>(r);
-          const i32x4 av = *reinterpret_cast<const i32x4*>(stage + r * ROW8 + ch * 16);
-          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], ks == 0 ? magic_c : c, 0, 0, 0);
+          const i32x4 av = *reinterpret_cast<const i32x4*>(stage + (kbase8 ^ (32 * ks)) + kb * 32 * ROW8);
+          c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], ks == 0 ? (kMagicC ? magic_c : (i32x16){}) : c, 0, 0, 0);
         }
         if (DUMP && a.dump_i32 != nullptr && row_ok) {
 #pragma unroll
@@ -376,13 +399,13 @@ attn32_kernel(const AttnKArgs a) {
             const int key = key0 + kb * 32 + 8 * (rr >> 2) + 4 * hi + (rr & 3);
             if (key < Lk)
               a.dump_i32[(int64_t)(q_start + row) * a.dump_t + (int64_t)h * a.dump_h + key] =
-                  c[rr] - 0x4B400000;
+                  c[rr] + kBiasAdd - 0x4B400000;
           }
         }
 #pragma unroll
         for (int j = 0; j < 8; ++j)
-          s16[kb][j] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[2 * j]), ss, negms)),
-                               fp32_round(__builtin_fmaf(__int_as_float(c[2 * j + 1]), ss, negms)));
+          s16[kb][j] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[2 * j] + kBiasAdd), ss, negms)),
+                               fp32_round(__builtin_fmaf(__int_as_float(c[2 * j + 1] + kBiasAdd), ss, negms)));
       }
     }
     if (DUMP && a.dump_f16 != nullptr && row_ok) {
@@ -480,6 +503,9 @@ attn32_kernel(const AttnKArgs a) {
     const unsigned char* vst = stage + KBUF;
     const int j16 = lane & 15;
     const int g16 = (lane >> 4) & 1;
+    const int vrl = 4 * hi + (j16 >> 2);
+    int vbase = vrl * ROW16 + (((16 * (2 * g16 + ((j16 & 3) >> 1))) ^ (16 * swz_v32<ROW16>(vrl))) | (8 * (j16 & 1)));
+    asm volatile("" : "+v"(vbase));
 #pragma unroll
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
@@ -490,10 +516,7 @@ attn32_kernel(const AttnKArgs a) {
           // V[k0 + j/4][D0 + 4 (j%4)]; output lane i gets V[k0..k0+3][D0 + i].
 #pragma unroll
           for (int h2 = 0; h2 < 2; ++h2) {
-            const int vr = 16 * ks + 8 * h2 + 4 * hi + (j16 >> 2);
-            const int col = 32 * db + 16 * g16 + 4 * (j16 & 3);
-            const int ch = (col >> 3) ^ swz_v32<ROW16>(vr);
-            const unsigned char* p = vst + vr * ROW16 + ch * 16 + (col & 7) * 2;
+            const unsigned char* p = vst + (vbase ^ (64 * db)) + (16 * ks + 8 * h2) * ROW16;
             const f16x4 v4 = lds_read_tr16(p);
             av[4 * h2 + 0] = v4[0];
             av[4 * h2 + 1] = v4[1];
