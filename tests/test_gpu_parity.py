@@ -234,6 +234,24 @@ def test_routing_modes_agree_with_maps(device):
     assert torch.equal(o_mix0, o_fp16)
 
 
+def test_run_length_merge_is_identity(device):
+    """run_length=True (reference :833-842) only merges consecutive mask groups
+    of the same route into one loop over the same tiles in the same order:
+    bitwise the same output as run_length=False, on a map with runs."""
+    lengths, hq, hk, d = [700, 1024], 4, 2, 128
+    q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=21)
+    qd, kd, vd, cud = (to_dev(a, device) for a in (q, k, v, cu))
+    mb = 8
+    rows = [0b1100111000011110, 0b1, 0xFFFF, 0b0110, 0b111000111, 0, 0b10, 0b11110000] * hk
+    bm = bitmask_tensor(rows[:hk * mb], device)
+    kw = dict(block_m=128, block_n=64, block_n_mask=128, causal=True, routing_mode="mixed",
+              int8_use_fp16_v=True)
+    o0, _ = tmx.tilemix_attention_with_quant(qd, kd, vd, cud, cud, 1024, 1024, bm, run_length=False, **kw)
+    o1, _ = tmx.tilemix_attention_with_quant(qd, kd, vd, cud, cud, 1024, 1024, bm, run_length=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(o0, o1)
+
+
 def test_varlen_dense_entry(device):
     """tilemix_varlen_attention([B,H,T,D]) == packed call; output is the permuted view."""
     from tilemix_amd.attention.tilemix_varlen import tilemix_varlen_attention
