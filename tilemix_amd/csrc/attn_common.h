@@ -94,6 +94,15 @@ __device__ __forceinline__ uint32_t pk_max(uint32_t x, uint32_t y) {
   return r;
 }
 
+// Packed fp16 maximum of three (IEEE maximum: the scores are never NaN for
+// finite inputs, and the sign of a zero maximum does not reach the results:
+// exp2(s - m) and exp2(m_old - m_new) are the same for m = +0 and -0).
+__device__ __forceinline__ uint32_t pk_max3(uint32_t x, uint32_t y, uint32_t z) {
+  uint32_t r;
+  asm("v_pk_maximum3_f16 %0, %1, %2, %3" : "=v"(r) : "v"(x), "v"(y), "v"(z));
+  return r;
+}
+
 // Materialise an fp32 value.  The reference rounds to fp32 and then to fp16
 // (Triton: mul.f32 / fma, then cvt.rn.f16.f32); without this barrier the
 // compiler fuses fptrunc(fma(a, b, c)) / fptrunc(fmul(a, b)) into one

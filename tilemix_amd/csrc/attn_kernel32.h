@@ -449,11 +449,11 @@ attn32_kernel(const AttnKArgs a) {
     }
 
     // ---- online softmax (reference _softmax_prefix_update) -------------
-    uint32_t t8[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) t8[j] = pk_max(s16[0][j], s16[1][j]);
-    const f16x2 mx2 = __builtin_bit_cast(
-        f16x2, pk_max(pk_max(pk_max(t8[0], t8[1]), pk_max(t8[2], t8[3])), pk_max(pk_max(t8[4], t8[5]), pk_max(t8[6], t8[7]))));
+    // 16 packed pairs -> 1 in 8 three-input maxima.
+    const uint32_t u0 = pk_max3(s16[0][0], s16[0][1], s16[0][2]), u1 = pk_max3(s16[0][3], s16[0][4], s16[0][5]);
+    const uint32_t u2 = pk_max3(s16[0][6], s16[0][7], s16[1][0]), u3 = pk_max3(s16[1][1], s16[1][2], s16[1][3]);
+    const uint32_t u4 = pk_max3(s16[1][4], s16[1][5], s16[1][6]);
+    const f16x2 mx2 = __builtin_bit_cast(f16x2, pk_max(pk_max3(u0, u1, u2), pk_max3(u3, u4, s16[1][7])));
     float mx = fmaxf((float)mx2[0], (float)mx2[1]);
     {
       const float2 sw = swap_halves(mx);
