@@ -103,6 +103,30 @@ __device__ __forceinline__ uint32_t pk_max3(uint32_t x, uint32_t y, uint32_t z) 
   return r;
 }
 
+// Eight int8 codes (bytes of w[0], then w[1]) to fp16, exactly: with the
+// sign bit flipped a code b is the byte u = b + 128, the fp16 with bits
+// 0x64XX is 1024 + u, and 1024 + u - 1152 = b (all exact small integers).
+// One byte permute builds two fp16 values, one packed add unbiases them.
+__device__ __forceinline__ f16x8 int8x8_to_f16(i32x2 w) {
+  const uint32_t w0 = (uint32_t)w[0] ^ 0x80808080u, w1 = (uint32_t)w[1] ^ 0x80808080u;
+  const f16x2 bias = {(f16)-1152.0f, (f16)-1152.0f};
+  // v_perm_b32: selector byte k < 4 picks byte k of the second source, k = 4
+  // picks byte 0 of the first (0x64).  (A plain array, not a vector: clang
+  // bit-casts an element of a vector variable from the vector's first bytes.)
+  const uint32_t r[4] = {__builtin_amdgcn_perm(0x64646464u, w0, 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, w0, 0x04030402u),
+                         __builtin_amdgcn_perm(0x64646464u, w1, 0x04010400u),
+                         __builtin_amdgcn_perm(0x64646464u, w1, 0x04030402u)};
+  f16x8 out;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const f16x2 v = __builtin_bit_cast(f16x2, r[i]) + bias;
+    out[2 * i] = v[0];
+    out[2 * i + 1] = v[1];
+  }
+  return out;
+}
+
 // Materialise an fp32 value.  The reference rounds to fp32 and then to fp16
 // (Triton: mul.f32 / fma, then cvt.rn.f16.f32); without this barrier the
 // compiler fuses fptrunc(fma(a, b, c)) / fptrunc(fmul(a, b)) into one

@@ -459,8 +459,7 @@ attn16_kernel(const AttnKArgs a) {
           const int vr = 32 * ks + 4 * lg + (b & 3) + 16 * (b >> 2);
           const int ch = db ^ swz_v8<ROW8>(vr);
           const i32x2 w = lds_read_tr8(vst + vr * ROW8 + ch * 16 + 8 * (li & 1));
-#pragma unroll
-          for (int e = 0; e < 8; ++e) av[e] = (f16)(float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
+          av = int8x8_to_f16(w);
         }
         acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[db], 0, 0, 0);
       }

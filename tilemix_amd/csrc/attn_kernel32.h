@@ -532,8 +532,7 @@ attn32_kernel(const AttnKArgs a) {
           const int ch = (col >> 4) ^ swz_k<ROW8>(vr);
           const unsigned char* p = vst + vr * ROW8 + ch * 16 + (col & 15);
           const i32x2 w = lds_read_tr8(p);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) av[e] = (f16)(float)(int8_t)((w[e >> 2] >> (8 * (e & 3))) & 0xff);
+          av = int8x8_to_f16(w);
         }
         const f16x8 pb = __builtin_bit_cast(f16x8, pv[ks]);
         acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb, acc[db], 0, 0, 0);
