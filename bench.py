@@ -51,6 +51,15 @@ def algorithmic_ops(b=B, hq=HQ, d=D, l=L) -> float:
     return 4.0 * b * hq * d * l * (l + 1) / 2.0
 
 
+def executed_tile_ops(b=B, hq=HQ, d=D, l=L, block_m=128) -> float:
+    """Ops of the 64-key tiles the kernel executes (whole tiles up to the
+    diagonal, masked lanes included): reported beside the algorithmic count,
+    never used as the roofline basis."""
+    nt = (l + 63) // 64
+    tiles = sum(min(nt, ((m + 1) * block_m + 63) // 64) for m in range((l + block_m - 1) // block_m))
+    return 4.0 * b * hq * d * block_m * 64 * tiles
+
+
 def int8_fraction(bitmask_row, l=L, block_m=128, block_n_mask=64) -> float:
     """Fraction of causally executed 64-key tiles routed to INT8."""
     nt = (l + 63) // 64
@@ -424,6 +433,8 @@ def main() -> int:
             "speedup_vs_all_fp16_map_kernel": k_ms_fp16map / k_ms,
             "speedup_vs_all_fp16_map_step": ms_fp16map / ms,
             "quant_plus_launch_ms": ms - k_ms,
+            "executed_tile_ops": executed_tile_ops(),
+            "executed_tile_tops_kernel": executed_tile_ops() / (k_ms * 1e-3) / 1e12,
             "step_ms_q_prepass": ms_prepass,
             "sweep": sweep,
             "other_configs": others,
