@@ -317,10 +317,12 @@ def test_in_kernel_q_quant_bitexact(device, case, monkeypatch):
 
 
 @pytest.mark.parametrize("block_m", [64, 128])
-def test_queries_shorter_than_keys(device, block_m):
-    """Separate cu_seqlens for Q and K (a query suffix over a longer key
-    prefix): the causal limit of row r is key r + Lk - Lq (reference :256-262)."""
-    pairs = [(100, 300), (300, 300), (1, 64), (200, 257)]
+def test_separate_q_and_k_lengths(device, block_m):
+    """Separate cu_seqlens for Q and K: the causal limit of row r is key
+    r + Lk - Lq (reference :256-262). Lq < Lk is a query suffix over a longer
+    key prefix; with Lq > Lk the first Lq - Lk rows (and every row of a
+    sequence without keys) see no key and stay 0 (acc 0, l 1)."""
+    pairs = [(100, 300), (300, 300), (1, 64), (200, 257), (300, 100), (130, 1), (64, 0)]
     hq, hk, d = 4, 2, 128
     rng = np.random.default_rng(41)
     lq = [p[0] for p in pairs]
