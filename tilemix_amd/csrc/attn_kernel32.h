@@ -23,7 +23,7 @@
 //   * O^T = V^T . P^T uses the S^T register layout directly as the B operand;
 //     the A operand (V^T) is read from row-major V with ds_read_b64_tr_b16;
 //   * K (fp16 or int8, by the tile's route) and V tiles are streamed straight
-//     from HBM into double-buffered LDS with global_load_lds_dwordx4 (no
+//     from HBM into double-buffered LDS with buffer_load_dwordx4 ... lds (no
 //     staging registers), in XOR-swizzled layouts that make every LDS read
 //     pattern of the MFMA operands bank-conflict free;
 //   * INT8 tiles accumulate on top of a magic bias (1.5*2^23 as int bits) so
@@ -229,6 +229,9 @@ attn32_kernel(const AttnKArgs a) {
     const int rem = Lk - key0;  // >= 1
     if (route == 0) {
       const SRsrc rs = make_srsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
+      // Opaque copy of the lane offset: the per-copy sums are formed here, one
+      // add each, instead of being hoisted into loop-invariant VGPRs (the
+      // same for the LDS read bases below).
       int o = dma_k16;
       asm volatile("" : "+v"(o));
 #pragma unroll
