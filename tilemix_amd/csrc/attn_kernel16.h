@@ -401,10 +401,12 @@ attn16_kernel(const AttnKArgs a) {
         ls = __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2, p16[kb][j]), ones, ls, false);
       }
     l_part = l_part * alpha + ls;
+    // alpha == 1 makes the reference's rescale an exact no-op, and so does a
+    // row that has seen no valid key yet (acc is still 0): skip it when one of
+    // the two holds for every row of the wave (always on a wave's first tile).
+    const bool rescale_noop = alpha == 1.0f || m_i == -INFINITY;
     m_i = m_next;
-    // alpha == 1 makes the reference's rescale an exact no-op: skip it when
-    // it holds for every row of the wave.
-    if (!__all(alpha == 1.0f)) {
+    if (!__all(rescale_noop)) {
 #pragma unroll
       for (int db = 0; db < NDB; ++db) acc[db] *= alpha;
     }
