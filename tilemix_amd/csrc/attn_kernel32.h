@@ -484,17 +484,15 @@ attn32_kernel(const AttnKArgs a) {
       }
     // Per-lane share of the row sum (the row's two lanes are combined at the end).
     l_i = l_i * alpha + ls;
-    // alpha == 1 makes the reference's rescale an exact no-op, and so does a
-    // row that has seen no valid key yet (acc is still 0): skip it when one of
-    // the two holds for every row of the wave (always on a wave's first tile).
-    const bool rescale_noop = alpha == 1.0f || m_i == -INFINITY;
     m_i = m_next;
-    if (!__all(rescale_noop)) {
+    // The rescale runs on every tile (alpha == 1 is an exact no-op). Skipping
+    // it when alpha == 1 on every row of the wave (a third of the tiles) made
+    // the register allocator copy the 64 accumulator VGPRs between the two
+    // paths on every tile, which cost more than the multiplies it saved.
 #pragma unroll
-      for (int db = 0; db < NDB; ++db)
+    for (int db = 0; db < NDB; ++db)
 #pragma unroll
-        for (int rr = 0; rr < 16; ++rr) acc[db][rr] *= alpha;
-    }
+      for (int rr = 0; rr < 16; ++rr) acc[db][rr] *= alpha;
 
     if (INT8V && route == 1) {
       // Reference :449-497: PV on int8 V codes with p scaled by the V block
