@@ -388,14 +388,19 @@ attn32_kernel(const AttnKArgs a) {
       const float negms = -kMagic * ss;
       int kbase8 = l32 * ROW8 + ((16 * hi) ^ (16 * swz_k<ROW8>(l32)));
       asm volatile("" : "+v"(kbase8));
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb) {
+      // Chain kb = 0 first; its dequant FMAs then run while the MFMAs of
+      // chain kb = 1 execute (the fences keep the compiler from interleaving
+      // the two chains, which would finish both at once).
+      auto qk8_chain = [&](int kb) -> i32x16 {
         i32x16 c;
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) {
           const i32x4 av = *reinterpret_cast<const i32x4*>(stage + (kbase8 ^ (32 * ks)) + kb * 32 * ROW8);
           c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], ks == 0 ? (kMagicC ? magic_c : (i32x16){}) : c, 0, 0, 0);
         }
+        return c;
+      };
+      auto dequant = [&](int kb, const i32x16& c) {
         if (DUMP && a.dump_i32 != nullptr && row_ok) {
 #pragma unroll
           for (int rr = 0; rr < 16; ++rr) {
@@ -409,7 +414,13 @@ attn32_kernel(const AttnKArgs a) {
         for (int j = 0; j < 8; ++j)
           s16[kb][j] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[2 * j] + kBiasAdd), ss, negms)),
                                fp32_round(__builtin_fmaf(__int_as_float(c[2 * j + 1] + kBiasAdd), ss, negms)));
-      }
+      };
+      const i32x16 c0 = qk8_chain(0);
+      __builtin_amdgcn_sched_barrier(0);
+      const i32x16 c1 = qk8_chain(1);
+      dequant(0, c0);
+      __builtin_amdgcn_sched_barrier(0);
+      dequant(1, c1);
     }
     if (DUMP && a.dump_f16 != nullptr && row_ok) {
 #pragma unroll
