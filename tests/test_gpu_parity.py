@@ -81,6 +81,10 @@ ATTN_CASES = [
     ("int8_v", [300], 4, 2, 128, 128, 64, True, "mixed", False, "rand"),
     ("hd80", [200], 2, 1, 80, 64, 64, True, "mixed", True, "rand"),
     ("gqa4_d64_bm128", [700], 8, 2, 64, 128, 64, True, "mixed", True, "rand"),
+    # int8 V codes in the 16-row kernel (block_m 64) and the 64-wide layouts
+    ("int8_v_bm64", [300, 129], 4, 2, 128, 64, 64, True, "mixed", False, "rand"),
+    ("int8_v_d64_bm64", [200, 77], 4, 1, 64, 64, 64, True, "int8", False, "rand"),
+    ("int8_v_d64_bm128", [333], 4, 2, 64, 128, 64, True, "mixed", False, "rand"),
 ]
 
 
