@@ -85,6 +85,9 @@ ATTN_CASES = [
     ("int8_v_bm64", [300, 129], 4, 2, 128, 64, 64, True, "mixed", False, "rand"),
     ("int8_v_d64_bm64", [200, 77], 4, 1, 64, 64, 64, True, "int8", False, "rand"),
     ("int8_v_d64_bm128", [333], 4, 2, 64, 128, 64, True, "mixed", False, "rand"),
+    # the specialised fp16 / int8 modes in the 16-row kernel
+    ("fp16_mode_bm64", [250, 64], 4, 2, 128, 64, 64, True, "fp16", True, "rand"),
+    ("int8_mode_bm64", [250, 64], 4, 2, 128, 64, 64, True, "int8", True, "rand"),
 ]
 
 
