@@ -157,13 +157,18 @@ def test_attention_outlier_channels(device, case):
         assert diff.max() <= 2e-3
 
 
-def test_attention_bias(device):
-    """Additive fp16 bias (reference :264-272), batch-0 bias applied to every sequence."""
-    lengths, hq, hk, d = [192, 192], 2, 1, 64
+@pytest.mark.parametrize("block_m,d,int8v", [(64, 64, True), (128, 128, True), (128, 128, False)])
+def test_attention_bias(device, block_m, d, int8v):
+    """Additive fp16 bias (reference :264-272), batch-0 bias applied to every
+    sequence; both kernels (block_m 64 / 128) and the int8-V variant."""
+    lengths, hq, hk = [192, 192], 2, 1
     rng = np.random.default_rng(4)
     bias = (rng.standard_normal((2, hq, 192, 192)) * 2).astype(np.float16)
     for mode in ("mixed", "fp16", "int8"):
-        got, ref, _ = _run_case(device, lengths, hq, hk, d, 64, 64, True, mode, True, "rand", seed=21, bias=bias)
+        if mode == "fp16" and not int8v:
+            continue  # the fp16 mode reads no V codes
+        got, ref, _ = _run_case(device, lengths, hq, hk, d, block_m, 64, True, mode, int8v, "rand", seed=21,
+                                bias=bias)
         assert_close_out(got, ref)
 
 
