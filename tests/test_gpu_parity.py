@@ -81,13 +81,21 @@ ATTN_CASES = [
     ("int8_v", [300], 4, 2, 128, 128, 64, True, "mixed", False, "rand"),
     ("hd80", [200], 2, 1, 80, 64, 64, True, "mixed", True, "rand"),
     ("gqa4_d64_bm128", [700], 8, 2, 64, 128, 64, True, "mixed", True, "rand"),
-    # int8 V codes in the 16-row kernel (block_m 64) and the 64-wide layouts
+    # int8 V codes: mixed routing in the 16-row kernel (block_m 64), int8
+    # routing at block_m 64 in the 32-row kernel, and the 64-wide layouts
     ("int8_v_bm64", [300, 129], 4, 2, 128, 64, 64, True, "mixed", False, "rand"),
     ("int8_v_d64_bm64", [200, 77], 4, 1, 64, 64, 64, True, "int8", False, "rand"),
     ("int8_v_d64_bm128", [333], 4, 2, 64, 128, 64, True, "mixed", False, "rand"),
-    # the specialised fp16 / int8 modes in the 16-row kernel
+    # the specialised fp16 / int8 modes at block_m 64 (128-row workgroups)
     ("fp16_mode_bm64", [250, 64], 4, 2, 128, 64, 64, True, "fp16", True, "rand"),
     ("int8_mode_bm64", [250, 64], 4, 2, 128, 64, 64, True, "int8", True, "rand"),
+    # mixed routing at block_m 64 on fp16 V: 128-row workgroups whose halves
+    # follow different routing blocks (both K formats staged where they differ);
+    # lengths 1, 50 and 129 leave the high half of a workgroup past the end
+    ("mixed_d128_bm64_ragged", [1, 50, 70, 129, 300, 64], 4, 2, 128, 64, 64, True, "mixed", True, "rand"),
+    ("mask_group2_bm64", [600], 4, 1, 128, 64, 128, True, "mixed", True, "rand"),
+    ("noncausal_d128_bm64", [200, 100], 2, 1, 128, 64, 64, False, "mixed", True, "rand"),
+    ("gqa4_d64_bm64", [450], 8, 2, 64, 64, 64, True, "mixed", True, "rand"),
 ]
 
 
@@ -157,10 +165,12 @@ def test_attention_outlier_channels(device, case):
         assert diff.max() <= 2e-3
 
 
-@pytest.mark.parametrize("block_m,d,int8v", [(64, 64, True), (128, 128, True), (128, 128, False)])
+@pytest.mark.parametrize("block_m,d,int8v", [(64, 64, True), (64, 128, True), (64, 128, False), (128, 128, True),
+                                              (128, 128, False)])
 def test_attention_bias(device, block_m, d, int8v):
     """Additive fp16 bias (reference :264-272), batch-0 bias applied to every
-    sequence; both kernels (block_m 64 / 128) and the int8-V variant."""
+    sequence; block_m 64 and 128 with fp16 and int8 V codes (int8v here is
+    int8_use_fp16_v: False runs the int8 V codes)."""
     lengths, hq, hk = [192, 192], 2, 1
     rng = np.random.default_rng(4)
     bias = (rng.standard_normal((2, hq, 192, 192)) * 2).astype(np.float16)
@@ -290,8 +300,9 @@ def test_varlen_dense_entry(device):
     assert_close_out(got, ref)
 
 
-# ------------------------------------------- in-kernel Q quantisation (block_m 128)
-FUSED_CASES = [c for c in ATTN_CASES if c[5] == 128 and c[8] != "fp16"]
+# ------------------------------- in-kernel Q quantisation (128-row workgroups)
+# Every case but block_m 64 with mixed routing on int8 V codes.
+FUSED_CASES = [c for c in ATTN_CASES if c[8] != "fp16" and (c[5] == 128 or c[9] or c[8] != "mixed")]
 
 
 @pytest.mark.parametrize("case", FUSED_CASES, ids=[c[0] for c in FUSED_CASES])
@@ -319,7 +330,7 @@ def test_in_kernel_q_quant_bitexact(device, case, monkeypatch):
     # the public entry: fused (default) vs pre-pass path
     args = (dq, dk, dv, dcu, dcu, max_len, max_len, bitmask_tensor(bits, device))
     ekw = dict(block_m=block_m, block_n=64, block_n_mask=bnm, BLKQ=128, BLKK=64, causal=causal,
-               routing_mode=mode, int8_use_fp16_v=int8v)
+               routing_mode=mode, int8_use_fp16_v=int8v, scalar_scales=(block_m == 128))
     monkeypatch.setenv("TILEMIX_HIP_FUSED_Q_QUANT", "0")
     out_pre, _ = tmx.tilemix_attention_with_quant(*args, **ekw)
     monkeypatch.setenv("TILEMIX_HIP_FUSED_Q_QUANT", "1")

@@ -124,6 +124,16 @@ def test_attn_validation_messages(lib):
     p.stride_k_token = p.stride_v_token = 1 << 25  # 64 MiB per token
     assert lib.tilemix_attn_fwd(ctypes.byref(p), None) == 1
     assert b"exceeds 2 GiB" in lib.tilemix_last_error()
+    # In-kernel Q quantisation needs 128-row workgroups: block_m 64 with mixed
+    # routing on int8 V codes runs 64-row workgroups.
+    p.stride_k_token = p.stride_v_token = 128
+    p.routing_mode, p.block_m, p.blkq, p.blkk = 0, 64, 128, 64
+    p.q_quant_in_kernel, p.int8_use_fp16_v = 1, 0
+    assert lib.tilemix_attn_fwd(ctypes.byref(p), None) == 1
+    assert b"128-row workgroups" in lib.tilemix_last_error()
+    p.blkq = 64
+    assert lib.tilemix_attn_fwd(ctypes.byref(p), None) == 1
+    assert b"128-row workgroups" in lib.tilemix_last_error()
 
 
 def test_quant_validation_messages(lib):
@@ -246,3 +256,14 @@ def test_varlen_entry_validates_before_launch():
         tilemix_varlen_attention(q[..., :32], k, k, 64, 64, precision_map_all=pm, **kw)
     with pytest.raises(ValueError, match="Bias shape mismatch"):
         tilemix_varlen_attention(q, k, k, 64, 64, precision_map_all=pm, bias=torch.zeros(1, 4, 256, 255), **kw)
+
+
+def test_q_in_kernel_rule():
+    """In-kernel Q quantisation needs a 128-row workgroup that is one BLKQ = 128
+    block: block_m 128, or block_m 64 unless mixed routing runs on int8 V codes."""
+    mixed, int8 = tmx.ROUTING_MODE_MIXED, tmx.ROUTING_MODE_INT8
+    assert tmx._q_in_kernel_supported(128, 128, mixed, False)
+    assert tmx._q_in_kernel_supported(64, 128, mixed, True)
+    assert tmx._q_in_kernel_supported(64, 128, int8, False)
+    assert not tmx._q_in_kernel_supported(64, 128, mixed, False)
+    assert not tmx._q_in_kernel_supported(128, 64, mixed, True)

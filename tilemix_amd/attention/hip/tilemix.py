@@ -248,8 +248,9 @@ def launch_prequantized(
     if (q8 is not None and q8.dtype != torch.int8) or k8.dtype != torch.int8:
         raise TypeError("q8 and k8 must be torch.int8")
     q_in_kernel = bool(_q_in_kernel) and mode_code != ROUTING_MODE_FP16
-    if q_in_kernel and (block_m != 128 or BLKQ != 128):
-        raise ValueError("in-kernel Q quantisation needs block_m == BLKQ == 128")
+    if q_in_kernel and not _q_in_kernel_supported(block_m, BLKQ, mode_code, int8_use_fp16_v):
+        raise ValueError("in-kernel Q quantisation needs BLKQ == 128 and 128-row workgroups "
+                         "(block_m 128, or block_m 64 without mixed routing on int8 V codes)")
     if mode_code != ROUTING_MODE_FP16 and not q_in_kernel and (q8 is None or sQ_blocks is None
                                                                 or cu_q_scale is None):
         raise ValueError("q8, sQ_blocks and cu_q_scale are required")
@@ -378,7 +379,8 @@ def tilemix_attention_with_quant(
     else:
         if not q.is_cuda:
             raise RuntimeError("TileMix is a GPU-only HIP kernel")
-        fused = _q_in_kernel_enabled() and block_m == 128 and BLKQ == 128
+        fused = _q_in_kernel_enabled() and _q_in_kernel_supported(
+            block_m, BLKQ, _routing_mode_code(normalized_mode), int8_use_fp16_v)
         if fused:
             q8 = sq = cuq = None
         else:
@@ -403,10 +405,18 @@ def tilemix_attention_with_quant(
     )
 
 
+def _q_in_kernel_supported(block_m: int, BLKQ: int, mode_code: int, int8_use_fp16_v: bool) -> bool:
+    """The kernel quantises Q per 128-row workgroup, which is one BLKQ = 128
+    block: block_m 128, and block_m 64 except with mixed routing on int8 V
+    codes (that variant runs 64-row workgroups)."""
+    wg128 = block_m == 128 or bool(int8_use_fp16_v) or mode_code != ROUTING_MODE_MIXED
+    return wg128 and BLKQ == 128
+
+
 def _q_in_kernel_enabled() -> bool:
-    """``TILEMIX_HIP_FUSED_Q_QUANT`` (default 1): with block_m == BLKQ == 128 the
-    attention kernel quantises Q itself instead of a separate pre-pass (same
-    codes and scales, bit for bit)."""
+    """``TILEMIX_HIP_FUSED_Q_QUANT`` (default 1): with BLKQ == 128 and 128-row
+    workgroups the attention kernel quantises Q itself instead of a separate
+    pre-pass (same codes and scales, bit for bit)."""
     return os.environ.get("TILEMIX_HIP_FUSED_Q_QUANT", "1").strip() not in ("0", "false", "False", "")
 
 

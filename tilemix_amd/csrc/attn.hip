@@ -55,6 +55,15 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   }
   const bool need_int8 = p.routing_mode != TILEMIX_ROUTING_FP16;
   const bool int8v = need_int8 && !p.int8_use_fp16_v;
+  // Kernel choice.  Every row's result depends only on its own route bits, so
+  // block_m = 64 runs on the 128-row workgroups of the 32-row kernel: with
+  // fp16 or int8 routing the map is not read, with mixed routing each half of
+  // the workgroup reads its own routing block.  Only mixed routing with int8 V
+  // (which has no room for both K formats in LDS) keeps 64-row workgroups.
+  const int kind = p.block_m == 128 ? kAttn32
+                 : p.routing_mode != TILEMIX_ROUTING_MIXED ? kAttn32
+                 : int8v ? kAttn16 : kAttn32Split;
+  const int wg_rows = kind == kAttn16 ? 64 : 128;
   if (p.routing_mode == TILEMIX_ROUTING_MIXED && !p.precision_bitmask) {
     set_error("%s: mixed routing needs precision_bitmask", fn);
     return TILEMIX_E_INVALID;
@@ -62,9 +71,10 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   // Tiles are streamed as 16-byte vectors: 16-byte aligned bases and strides.
   if (need_int8) {
     if (p.q_quant_in_kernel) {
-      if (p.block_m != 128 || p.blkq != 128) {
-        set_error("%s: q_quant_in_kernel needs block_m == BLKQ == 128 (block_m=%d, BLKQ=%d)", fn, p.block_m,
-                  p.blkq);
+      // The workgroup quantises its own 128 rows: one BLKQ = 128 block.
+      if (wg_rows != 128 || p.blkq != 128) {
+        set_error("%s: q_quant_in_kernel needs BLKQ == 128 and 128-row workgroups (block_m 128, or block_m 64 "
+                  "without mixed int8-V routing); block_m=%d, BLKQ=%d", fn, p.block_m, p.blkq);
         return TILEMIX_E_INVALID;
       }
     } else if (!p.q8 || !p.sq || !p.cu_q_scale) {
@@ -122,7 +132,7 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
     return TILEMIX_E_INVALID;
   }
 
-  const int m_blocks = (p.max_seqlen_q + p.block_m - 1) / p.block_m;
+  const int m_blocks = (p.max_seqlen_q + wg_rows - 1) / wg_rows;
   const int64_t total = (int64_t)m_blocks * p.heads_q * p.batch;
   if (total == 0) return TILEMIX_OK;
   if (total > (int64_t)1 << 30) {
@@ -185,7 +195,7 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.per_xcd = (int)work_items_per_xcd((int64_t)p.heads_k * p.batch, (int64_t)m_blocks * a.group);
 
   const int dp = p.head_dim <= 64 ? 64 : 128;
-  dispatch_attn(a, p.block_m, dp, p.routing_mode, int8v, dump, p.bias != nullptr, stream);
+  dispatch_attn(a, kind, dp, p.routing_mode, int8v, dump, p.bias != nullptr, stream);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     set_error("%s: launch failed: %s", fn, hipGetErrorString(err));
@@ -198,15 +208,15 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
 
 namespace tmx {
 
-void dispatch_attn_main(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, hipStream_t stream);
-void dispatch_attn_bias(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, hipStream_t stream);
-void dispatch_attn_dump(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_main(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_bias(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_dump(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
 
-void dispatch_attn(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, bool dump, bool bias,
+void dispatch_attn(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, bool dump, bool bias,
                    hipStream_t stream) {
-  if (dump) dispatch_attn_dump(a, block_m, dp, mode, int8v, stream);
-  else if (bias) dispatch_attn_bias(a, block_m, dp, mode, int8v, stream);
-  else dispatch_attn_main(a, block_m, dp, mode, int8v, stream);
+  if (dump) dispatch_attn_dump(a, kind, dp, mode, int8v, stream);
+  else if (bias) dispatch_attn_bias(a, kind, dp, mode, int8v, stream);
+  else dispatch_attn_main(a, kind, dp, mode, int8v, stream);
 }
 
 }  // namespace tmx

@@ -36,11 +36,11 @@ struct AttnKArgs {
   int64_t dump_t, dump_h;
   float qk_scale;
   int hq, hk, group, d;
-  int m_blocks;   // ceil(max_seqlen_q / block_m)
+  int m_blocks;   // ceil(max_seqlen_q / rows per workgroup)
   int mask_tiles; // block_n_mask / block_n
   int blkq, blkk;
   int causal;
-  int q_fused;      // Q quantised in the attention kernel (block_m == BLKQ == 128)
+  int q_fused;      // Q quantised in the attention kernel (128-row workgroups, BLKQ == 128)
   int total_items;  // (sequence, query head, query block) work items
   int per_xcd;
 };
@@ -243,8 +243,15 @@ __device__ __forceinline__ int swz_v8(int r) {
   else return (r >> 2) & 3;  // 64-byte rows
 }
 
+// Which kernel runs a launch (chosen in launch_attn).
+enum AttnKind : int {
+  kAttn32 = 0,       // 32-row kernel, one routing block per 128-row workgroup
+  kAttn32Split = 1,  // 32-row kernel, two 64-row routing blocks per workgroup
+  kAttn16 = 2,       // 16-row kernel, one 64-row routing block per workgroup
+};
+
 // Launch one instantiation (defined in attn_inst_*.hip).
-void dispatch_attn(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, bool dump, bool bias,
+void dispatch_attn(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, bool dump, bool bias,
                    hipStream_t stream);
 
 }  // namespace tmx

@@ -3,8 +3,8 @@
 
 namespace tmx {
 
-void dispatch_attn_dump(const AttnKArgs& a, int block_m, int dp, int mode, bool int8v, hipStream_t stream) {
-  AttnLauncher<true, false>::run(a, block_m, dp, mode, int8v, stream);
+void dispatch_attn_dump(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream) {
+  AttnLauncher<true, false>::run(a, kind, dp, mode, int8v, stream);
 }
 
 }  // namespace tmx

@@ -1,5 +1,8 @@
 // Fused FP16/INT8-routed flash-attention prefill forward for gfx950: the
-// 32-row kernel (block_m = 128: 4 waves x 32 query rows).
+// 32-row kernel (4 waves x 32 query rows = 128 rows per workgroup).  It runs
+// block_m = 128 and, with SPLIT, block_m = 64: the workgroup's two 64-row
+// halves are two routing blocks, and a key tile whose route differs between
+// the halves is staged in both K formats.
 //
 // Numerics follow attn_fwd (attention/triton/tilemix.py:503-951):
 //   qk_scale = fp32(sm_scale) * fp32(log2 e)                               (:641)
@@ -39,9 +42,10 @@
 
 namespace tmx {
 
-template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS>
+template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS, bool SPLIT>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn32_kernel(const AttnKArgs a) {
+  static_assert(!SPLIT || (NW % 2 == 0 && !INT8V), "split workgroups: even wave count, fp16 V");
   constexpr int BM = NW * 32;
   constexpr int KS16 = DP / 16;  // fp16 MFMA k-steps (32x32x16)
   constexpr int KS8 = DP / 32;   // int8 MFMA k-steps (32x32x32)
@@ -50,7 +54,10 @@ attn32_kernel(const AttnKArgs a) {
   constexpr int ROW8 = DP;       // bytes per int8 row
   constexpr int KBUF = 64 * ROW16;               // K stage (fp16 or int8)
   constexpr int VBUF = 64 * ROW16;               // V stage (fp16; int8 V uses half)
-  constexpr int STAGE = KBUF + VBUF;
+  // A split stage holds K in both formats (int8 K after V); otherwise an
+  // int8 K tile takes the fp16 K slot.
+  constexpr int K8OFF = SPLIT ? KBUF + VBUF : 0;
+  constexpr int STAGE = KBUF + VBUF + (SPLIT ? 64 * ROW8 : 0);
   constexpr int K16_INS = KBUF / 1024 / NW;      // 1 KB wave loads per wave per tile
   constexpr int K8_INS = (64 * ROW8) / 1024 / NW;
   constexpr int V16_INS = VBUF / 1024 / NW;
@@ -58,7 +65,11 @@ attn32_kernel(const AttnKArgs a) {
   static_assert(K16_INS >= 1 && K8_INS >= 1 && V16_INS >= 1 && V8_INS >= 1, "tile split");
 
   __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE];
-  __shared__ float q_red[NW];  // per-wave partial max of the in-kernel Q quantisation
+  // Per-wave partial max of the in-kernel Q quantisation, in the last bytes of
+  // stage 1: that stage is first written after the loop's first barrier, when
+  // every wave has read these values.  (A separate array would push the split
+  // DP=128 workgroup past 80 KB and halve the workgroups per CU.)
+  float* const q_red = reinterpret_cast<float*>(smem + 2 * STAGE - 4 * NW);
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -93,11 +104,19 @@ attn32_kernel(const AttnKArgs a) {
   }
   const int diag = Lk - Lq;  // causal: key valid iff key <= row + diag
 
-  uint64_t bits = 0;
+  // Route bits of the workgroup's rows (SPLIT: bits of the low half, bits_hi
+  // of the high half; a high half past the sequence end takes the low half's).
+  uint64_t bits = 0, bits_hi = 0;
   if (MODE == TILEMIX_ROUTING_MIXED) {
-    const int mbz = (Lq + BM - 1) / BM;  // per-sequence m_blocks (reference :819-820)
-    bits = a.bitmask[hk * mbz + m];
+    constexpr int RB = SPLIT ? BM / 2 : BM;  // rows per routing block
+    const int mbz = (Lq + RB - 1) / RB;      // per-sequence m_blocks (reference :819-820)
+    const int mb = SPLIT ? 2 * m : m;
+    bits = a.bitmask[hk * mbz + mb];
+    if (SPLIT) bits_hi = mb + 1 < mbz ? a.bitmask[hk * mbz + mb + 1] : bits;
   }
+  // Last key any row of the low half attends to: later tiles need only the
+  // high half's format.
+  const int lo_last_key = a.causal ? m * BM + BM / 2 - 1 + Lk - Lq : Lk;
 
   const int row0w = m * BM + wave * 32;  // first row of this wave
   const int row = row0w + l32;            // this lane's query row
@@ -224,10 +243,13 @@ attn32_kernel(const AttnKArgs a) {
   const int step_v16 = NW * (1024 / ROW16) * (int)vt_bytes;
   const int step_v8 = NW * (1024 / ROW8) * (int)v8t_bytes;
   const uint32_t smem_lds = lds_addr(smem);
+  // route: 0 fp16 / 1 int8; SPLIT: bit 0 the low half's route, bit 1 the high half's.
   auto issue_tile = [&](int n, int route, uint32_t stage) {
     const int key0 = n * kBN;
     const int rem = Lk - key0;  // >= 1
-    if (route == 0) {
+    const bool need16 = MODE != TILEMIX_ROUTING_INT8 && (SPLIT ? route != 3 : route == 0);
+    const bool need8 = MODE != TILEMIX_ROUTING_FP16 && route != 0;
+    if (need16) {
       const SRsrc rs = make_srsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
       // Opaque copy of the lane offset: the per-copy sums are formed here, one
       // add each, instead of being hoisted into loop-invariant VGPRs (the
@@ -237,13 +259,14 @@ attn32_kernel(const AttnKArgs a) {
 #pragma unroll
       for (int i = 0; i < K16_INS; ++i)
         async_load16_asm(rs, o + i * step_k16, stage + (i * NW + wave) * 1024);
-    } else {
+    }
+    if (need8) {
       const SRsrc rs = make_srsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
       int o = dma_k8;
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < K8_INS; ++i)
-        async_load16_asm(rs, o + i * step_k8, stage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, o + i * step_k8, stage + K8OFF + (i * NW + wave) * 1024);
     }
     const uint32_t vstage = stage + KBUF;
     if (!INT8V || route == 0) {
@@ -280,11 +303,19 @@ attn32_kernel(const AttnKArgs a) {
   // Issues the next tile (index nx) and fetches its scales; the loads land
   // before the barrier that precedes the tile's compute.
   auto issue_next = [&](int nx, uint32_t stage, int& route, f16& skv, f16& svv) {
-    route = MODE == TILEMIX_ROUTING_FP16 ? 0
-          : MODE == TILEMIX_ROUTING_INT8 ? 1
-          : (int)((bits >> (unsigned)nx_grp) & 1ull);
+    if (MODE == TILEMIX_ROUTING_FP16) {
+      route = 0;
+    } else if (MODE == TILEMIX_ROUTING_INT8) {
+      route = SPLIT ? 3 : 1;
+    } else if (!SPLIT) {
+      route = (int)((bits >> (unsigned)nx_grp) & 1ull);
+    } else {
+      const int rhi = (int)((bits_hi >> (unsigned)nx_grp) & 1ull);
+      const int rlo = nx * kBN > lo_last_key ? rhi : (int)((bits >> (unsigned)nx_grp) & 1ull);
+      route = rlo | (rhi << 1);
+    }
     issue_tile(nx, route, stage);
-    if (MODE != TILEMIX_ROUTING_FP16 && route == 1) {
+    if (MODE != TILEMIX_ROUTING_FP16 && route != 0) {
       skv = (f16)1.0f;
       if (kend > kbase) skv = a.sk[(int64_t)min(kbase + nx_sb, kend - 1) * a.hk + hk];
       if (INT8V) {
@@ -331,8 +362,9 @@ attn32_kernel(const AttnKArgs a) {
   f16 sk_next = (f16)1.0f, sv_next = (f16)1.0f;
   if (n_blocks > 0) issue_next(0, smem_lds, route_next, sk_next, sv_next);
 
+  const int half = SPLIT && wave >= NW / 2 ? 1 : 0;
   for (int n = 0; n < n_blocks; ++n) {
-    const int route = route_next;
+    const int route = SPLIT ? (route_next >> half) & 1 : route_next;
     const f16 sk16 = sk_next;
     const f16 sv16 = sv_next;
     unsigned char* stage = smem + (n & 1) * STAGE;
@@ -395,7 +427,7 @@ attn32_kernel(const AttnKArgs a) {
         i32x16 c;
 #pragma unroll
         for (int ks = 0; ks < KS8; ++ks) {
-          const i32x4 av = *reinterpret_cast<const i32x4*>(stage + (kbase8 ^ (32 * ks)) + kb * 32 * ROW8);
+          const i32x4 av = *reinterpret_cast<const i32x4*>(stage + K8OFF + (kbase8 ^ (32 * ks)) + kb * 32 * ROW8);
           c = __builtin_amdgcn_mfma_i32_32x32x32_i8(av, q8f[ks], ks == 0 ? (kMagicC ? magic_c : (i32x16){}) : c, 0, 0, 0);
         }
         return c;
