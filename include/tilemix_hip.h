@@ -99,7 +99,8 @@ int tilemix_quant_per_block_int8(const tilemix_quant_params* p, void* stream);
  * tile group (block_n_mask keys) to FP16 or INT8 QK^T by bit j of
  * precision_bitmask[hk * ceil(Lq_z / block_m) + m] (hk = h / (heads_q/heads_k)).
  *
- * q_quant_in_kernel = 1 (block_m == blkq == 128, routing not FP16): each
+ * q_quant_in_kernel = 1 (blkq == 128, routing not FP16, and block_m == 128 or
+ * block_m == 64 unless mixed routing runs on int8 V codes): each 128-row
  * workgroup quantises its own 128-row Q block (scale = max|q|/127, code =
  * trunc(q/scale +- 0.5), exactly quant_per_block_int8 with sm_scale = 1, the
  * way tilemix_attention_with_quant quantises Q, tilemix.py:126-140) instead of
