@@ -53,10 +53,13 @@ attn32_kernel(const AttnKArgs a) {
   constexpr int ROW16 = DP * 2;  // bytes per fp16 row
   constexpr int ROW8 = DP;       // bytes per int8 row
   constexpr int KBUF = 64 * ROW16;               // K stage (fp16 or int8)
-  constexpr int VBUF = 64 * ROW16;               // V stage (fp16; int8 V uses half)
+  constexpr int VBUF = 64 * ROW16;               // V stage (fp16; int8 V codes are widened into it)
   // A split stage holds K in both formats (int8 K after V); otherwise an
   // int8 K tile takes the fp16 K slot.
   constexpr int K8OFF = SPLIT ? KBUF + VBUF : 0;
+  // int8 V codes land in the half of the K slot an int8 K tile leaves free and
+  // are widened to fp16 into the V slot before the tile's barrier.
+  constexpr int V8OFF = 64 * ROW8;
   constexpr int STAGE = KBUF + VBUF + (SPLIT ? 64 * ROW8 : 0);
   constexpr int K16_INS = KBUF / 1024 / NW;      // 1 KB wave loads per wave per tile
   constexpr int K8_INS = (64 * ROW8) / 1024 / NW;
@@ -282,7 +285,29 @@ attn32_kernel(const AttnKArgs a) {
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < V8_INS; ++i)
-        async_load16_asm(rs, o + i * step_v8, vstage + (i * NW + wave) * 1024);
+        async_load16_asm(rs, o + i * step_v8, stage + V8OFF + (i * NW + wave) * 1024);
+    }
+  };
+
+  // int8 V codes -> fp16 V tile (the layout of an fp16 V copy).  Each wave
+  // widens exactly the 1 KB pieces it copied itself, so its own vmcnt wait is
+  // enough; the tile's barrier then publishes the fp16 tile to every wave.
+  // One conversion per code and workgroup, instead of one per code and wave
+  // in the PV loop.
+  auto widen_v8 = [&](unsigned char* stg) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    constexpr int rpi = 1024 / ROW8, cpr = ROW8 / 16;
+#pragma unroll
+    for (int i = 0; i < V8_INS; ++i) {
+      const int r = (i * NW + wave) * rpi + lane / cpr;  // key row of this lane's 16 codes
+      const int cc = (lane % cpr) ^ swz_k<ROW8>(r);      // their 16-column chunk
+      const i32x4 w = *reinterpret_cast<const i32x4*>(stg + V8OFF + (i * NW + wave) * 1024 + lane * 16);
+      const f16x8 lo = int8x8_to_f16((i32x2){w[0], w[1]});
+      const f16x8 hi8 = int8x8_to_f16((i32x2){w[2], w[3]});
+      const int sv = swz_v32<ROW16>(r);
+      unsigned char* row = stg + KBUF + r * ROW16;
+      *reinterpret_cast<f16x8*>(row + (((2 * cc) ^ sv) * 16)) = lo;
+      *reinterpret_cast<f16x8*>(row + (((2 * cc + 1) ^ sv) * 16)) = hi8;
     }
   };
 
@@ -371,6 +396,7 @@ attn32_kernel(const AttnKArgs a) {
     // Tile n has landed (own loads), then every wave's loads have landed and
     // every wave is done with the other stage (tile n-1).
     __builtin_amdgcn_s_waitcnt(0);
+    if (INT8V && route == 1) widen_v8(stage);
     __syncthreads();
     if (n + 1 < n_blocks)
       issue_next(n + 1, smem_lds + ((n + 1) & 1) * STAGE, route_next, sk_next, sv_next);
@@ -556,29 +582,18 @@ attn32_kernel(const AttnKArgs a) {
     for (int db = 0; db < NDB; ++db) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) {
+        // ds_read_b64_tr_b16: in a 16-lane group, input lane j points at
+        // V[k0 + j/4][D0 + 4 (j%4)]; output lane i gets V[k0..k0+3][D0 + i]
+        // (int8 V codes were widened to this fp16 layout at the tile's start).
         f16x8 av;
-        if (!INT8V || route == 0) {
-          // ds_read_b64_tr_b16: in a 16-lane group, input lane j points at
-          // V[k0 + j/4][D0 + 4 (j%4)]; output lane i gets V[k0..k0+3][D0 + i].
 #pragma unroll
-          for (int h2 = 0; h2 < 2; ++h2) {
-            const unsigned char* p = vst + (vbase ^ (64 * db)) + (16 * ks + 8 * h2) * ROW16;
-            const f16x4 v4 = lds_read_tr16(p);
-            av[4 * h2 + 0] = v4[0];
-            av[4 * h2 + 1] = v4[1];
-            av[4 * h2 + 2] = v4[2];
-            av[4 * h2 + 3] = v4[3];
-          }
-        } else {
-          // int8 V codes, ds_read_b64_tr_b8: input lane j points at
-          // V8[k_{j/2}][D0 + 8 (j%2)]; output lane i gets V8[k_0..k_7][D0 + i].
-          const int jj = j16 >> 1;  // key slot t of this input lane
-          const int vr = 16 * ks + 8 * (jj >> 2) + 4 * hi + (jj & 3);
-          const int col = 32 * db + 16 * g16 + 8 * (j16 & 1);
-          const int ch = (col >> 4) ^ swz_k<ROW8>(vr);
-          const unsigned char* p = vst + vr * ROW8 + ch * 16 + (col & 15);
-          const i32x2 w = lds_read_tr8(p);
-          av = int8x8_to_f16(w);
+        for (int h2 = 0; h2 < 2; ++h2) {
+          const unsigned char* p = vst + (vbase ^ (64 * db)) + (16 * ks + 8 * h2) * ROW16;
+          const f16x4 v4 = lds_read_tr16(p);
+          av[4 * h2 + 0] = v4[0];
+          av[4 * h2 + 1] = v4[1];
+          av[4 * h2 + 2] = v4[2];
+          av[4 * h2 + 3] = v4[3];
         }
         const f16x8 pb = __builtin_bit_cast(f16x8, pv[ks]);
         acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb, acc[db], 0, 0, 0);
