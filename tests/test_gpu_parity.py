@@ -85,6 +85,7 @@ ATTN_CASES = [
     # routing at block_m 64 in the 32-row kernel, and the 64-wide layouts
     ("int8_v_bm64", [300, 129], 4, 2, 128, 64, 64, True, "mixed", False, "rand"),
     ("int8_v_d64_bm64", [200, 77], 4, 1, 64, 64, 64, True, "int8", False, "rand"),
+    ("int8_v_d64_bm64_mixed", [200, 77], 4, 1, 64, 64, 64, True, "mixed", False, "rand"),
     ("int8_v_d64_bm128", [333], 4, 2, 64, 128, 64, True, "mixed", False, "rand"),
     # the specialised fp16 / int8 modes at block_m 64 (128-row workgroups)
     ("fp16_mode_bm64", [250, 64], 4, 2, 128, 64, 64, True, "fp16", True, "rand"),

@@ -199,16 +199,11 @@ __device__ __forceinline__ void async_load16_asm(const SRsrc& rs, int voffset, u
       : "memory");
 }
 
-// Transposed LDS reads (gfx950).  tr16: within each 16-lane group, output lane
-// i, element c = element (i % 4) of the 8 bytes addressed by lane 4c + i/4.
-// tr8: output lane i, byte b = byte (i % 8) of the 8 bytes addressed by lane
-// 2b + i/8.
+// Transposed LDS read (gfx950): within each 16-lane group, output lane i,
+// element c = element (i % 4) of the 8 bytes addressed by lane 4c + i/4.
 __device__ __forceinline__ f16x4 lds_read_tr16(const unsigned char* p) {
   const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) s16x4*)p);
   return __builtin_bit_cast(f16x4, v);
-}
-__device__ __forceinline__ i32x2 lds_read_tr8(const unsigned char* p) {
-  return __builtin_amdgcn_ds_read_tr8_b64_v2i32((__attribute__((address_space(3))) i32x2*)p);
 }
 
 // ---- LDS layouts ----------------------------------------------------------
@@ -217,8 +212,8 @@ __device__ __forceinline__ i32x2 lds_read_tr8(const unsigned char* p) {
 // one LDS pass (16 lanes of ds_read_b128, 32 lanes of a transposed b64 read)
 // over all 64 banks:
 //   K fp16 / int8 (ds_read_b128): 16 lanes read one chunk of 16 consecutive rows;
-//   V fp16 (ds_read_b64_tr_b16): 32 lanes read 2 chunks of 8 consecutive rows;
-//   V int8 (ds_read_b64_tr_b8): 32 lanes read 1 chunk of rows {0..7, 16..23} + 32 ks.
+//   V fp16 (ds_read_b64_tr_b16): 32 lanes read 2 chunks of 8 consecutive rows.
+// int8 V codes are copied like int8 K (swz_k) and widened to the fp16 V layout.
 template <int ROWB>
 __device__ __forceinline__ int swz_k(int r) {
   if constexpr (ROWB >= 256) return r & 15;
@@ -236,11 +231,6 @@ template <int ROWB>
 __device__ __forceinline__ int swz_v32(int r) {
   if constexpr (ROWB >= 256) return 4 * (r & 3);
   else return 4 * ((r >> 1) & 1);  // 128-byte rows: row pairs share a bank line
-}
-template <int ROWB>
-__device__ __forceinline__ int swz_v8(int r) {
-  if constexpr (ROWB >= 128) return ((r >> 1) & 3) | ((r >> 2) & 4);
-  else return (r >> 2) & 3;  // 64-byte rows
 }
 
 // Which kernel runs a launch (chosen in launch_attn).

@@ -27,7 +27,7 @@
 //   * O^T = V^T . P^T takes P^T straight from those registers: the MFMA's k
 //     slots 8 (l/16) + t are mapped to keys 32 ks + 4 (l/16) + (t%4) + 16 (t/4),
 //     and the V^T operand is read in the same key order with two
-//     ds_read_b64_tr_b16 (one ds_read_b64_tr_b8 for int8 V codes);
+//     ds_read_b64_tr_b16 (int8 V codes are first widened to fp16 in LDS);
 //   * the row sum l is kept per lane (partial over the lane's keys, rescaled
 //     by the row's alpha) and combined across the row's 4 lanes once, at the end;
 //   * K (fp16 or int8, by the tile's route) and V tiles are streamed straight
@@ -57,8 +57,10 @@ attn16_kernel(const AttnKArgs a) {
   constexpr int ROW16 = DP * 2;  // bytes per fp16 row
   constexpr int ROW8 = DP;       // bytes per int8 row
   constexpr int KBUF = 64 * ROW16;  // K stage (fp16 or int8)
-  constexpr int VBUF = 64 * ROW16;  // V stage (fp16; int8 V uses half)
+  constexpr int VBUF = 64 * ROW16;  // V stage (fp16; int8 V codes are widened into it)
   constexpr int STAGE = KBUF + VBUF;
+  // int8 V codes land in the half of the K slot an int8 K tile leaves free.
+  constexpr int V8OFF = 64 * ROW8;
   // 1 KB wave loads per tile, and how many each wave issues.
   constexpr int K16_T = 64 * ROW16 / 1024, K8_T = 64 * ROW8 / 1024;
   constexpr int K16_I = (K16_T + NW - 1) / NW, K8_I = (K8_T + NW - 1) / NW;
@@ -169,13 +171,12 @@ attn16_kernel(const AttnKArgs a) {
       ? reinterpret_cast<const unsigned char*>(a.k8 + (int64_t)k_start * a.sk8_t + (int64_t)hk * a.sk8_h) : nullptr;
   const unsigned char* v8seq = INT8V
       ? reinterpret_cast<const unsigned char*>(a.v8 + (int64_t)k_start * a.sv8_t + (int64_t)hk * a.sv8_h) : nullptr;
-  // 0 = K (fp16 or int8), 1 = V fp16, 2 = V int8.
+  // 0 = K (fp16 or int8) and int8 V codes, 1 = V fp16.
   auto lane_off = [&](int L, int rowb, int64_t tok_bytes, int kind) -> int {
     const int rpi = 1024 / rowb, cpr = rowb / 16;
     const int r = L * rpi + lane / cpr;
     int sw;
     if (kind == 1) sw = rowb == 256 ? swz_v<256>(r) : swz_v<128>(r);
-    else if (kind == 2) sw = rowb == 128 ? swz_v8<128>(r) : swz_v8<64>(r);
     else sw = rowb == 256 ? swz_k<256>(r) : rowb == 128 ? swz_k<128>(r) : swz_k<64>(r);
     return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
   };
@@ -213,7 +214,30 @@ attn16_kernel(const AttnKArgs a) {
 #pragma unroll
       for (int i = 0; i < K8_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K8_T) async_load16_asm(rs, lane_off(L, ROW8, v8t_bytes, 2), vstage + L * 1024);
+        if (L < K8_T) async_load16_asm(rs, lane_off(L, ROW8, v8t_bytes, 0), stage + V8OFF + L * 1024);
+      }
+    }
+  };
+
+  // int8 V codes -> fp16 V tile (the layout of an fp16 V copy).  Each wave
+  // widens exactly the 1 KB pieces it copied itself, so its own vmcnt wait is
+  // enough; the tile's barrier then publishes the fp16 tile to every wave.
+  auto widen_v8 = [&](unsigned char* stg) {
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    constexpr int rpi = 1024 / ROW8, cpr = ROW8 / 16;
+#pragma unroll
+    for (int i = 0; i < K8_I; ++i) {
+      const int L = i * NW + wave;
+      if (L < K8_T) {
+        const int r = L * rpi + lane / cpr;               // key row of this lane's 16 codes
+        const int cc = (lane % cpr) ^ swz_k<ROW8>(r);     // their 16-column chunk
+        const i32x4 w = *reinterpret_cast<const i32x4*>(stg + V8OFF + L * 1024 + lane * 16);
+        const f16x8 lo = int8x8_to_f16((i32x2){w[0], w[1]});
+        const f16x8 hi8 = int8x8_to_f16((i32x2){w[2], w[3]});
+        const int sv = swz_v<ROW16>(r);
+        unsigned char* row = stg + KBUF + r * ROW16;
+        *reinterpret_cast<f16x8*>(row + (((2 * cc) ^ sv) * 16)) = lo;
+        *reinterpret_cast<f16x8*>(row + (((2 * cc + 1) ^ sv) * 16)) = hi8;
       }
     }
   };
@@ -251,6 +275,7 @@ attn16_kernel(const AttnKArgs a) {
     // Tile n has landed (own loads), then every wave's loads have landed and
     // every wave is done with the other stage (tile n-1).
     __builtin_amdgcn_s_waitcnt(0);
+    if (INT8V && route == 1) widen_v8(stage);
     __syncthreads();
     if (n + 1 < n_blocks) {
       route_next = route_of(n + 1);
@@ -438,30 +463,20 @@ attn16_kernel(const AttnKArgs a) {
         }
 #pragma unroll
       for (int db = 0; db < NDB; ++db) {
+        // tr16: input lane li points at V[k0 + li/4][16 db + 4 (li%4)];
+        // output lane li gets V[k0..k0+3][16 db + li] (int8 V codes were
+        // widened to this fp16 layout at the tile's start).
         f16x8 av;
-        if (!INT8V || route == 0) {
-          // tr16: input lane li points at V[k0 + li/4][16 db + 4 (li%4)];
-          // output lane li gets V[k0..k0+3][16 db + li].
 #pragma unroll
-          for (int hb = 0; hb < 2; ++hb) {
-            const int vr = 32 * ks + 16 * hb + 4 * lg + (li >> 2);
-            const int col = 16 * db + 4 * (li & 3);
-            const int ch = (col >> 3) ^ swz_v<ROW16>(vr);
-            const f16x4 v4 = lds_read_tr16(vst + vr * ROW16 + ch * 16 + (col & 7) * 2);
-            av[4 * hb + 0] = v4[0];
-            av[4 * hb + 1] = v4[1];
-            av[4 * hb + 2] = v4[2];
-            av[4 * hb + 3] = v4[3];
-          }
-        } else {
-          // tr8: lanes 2b, 2b+1 point at row R_b = 32 ks + 4 lg + (b%4) +
-          // 16 (b/4), bytes 16 db + 8 (li%2); output lane li byte b =
-          // V8[R_b][16 db + li].
-          const int b = li >> 1;
-          const int vr = 32 * ks + 4 * lg + (b & 3) + 16 * (b >> 2);
-          const int ch = db ^ swz_v8<ROW8>(vr);
-          const i32x2 w = lds_read_tr8(vst + vr * ROW8 + ch * 16 + 8 * (li & 1));
-          av = int8x8_to_f16(w);
+        for (int hb = 0; hb < 2; ++hb) {
+          const int vr = 32 * ks + 16 * hb + 4 * lg + (li >> 2);
+          const int col = 16 * db + 4 * (li & 3);
+          const int ch = (col >> 3) ^ swz_v<ROW16>(vr);
+          const f16x4 v4 = lds_read_tr16(vst + vr * ROW16 + ch * 16 + (col & 7) * 2);
+          av[4 * hb + 0] = v4[0];
+          av[4 * hb + 1] = v4[1];
+          av[4 * hb + 2] = v4[2];
+          av[4 * hb + 3] = v4[3];
         }
         acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[db], 0, 0, 0);
       }
