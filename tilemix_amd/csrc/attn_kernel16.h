@@ -1,4 +1,6 @@
-// Fused FP16/INT8-routed flash-attention prefill forward for gfx950 (kernel template).
+// Fused FP16/INT8-routed flash-attention prefill forward for gfx950: the
+// 16-row kernel, which runs block_m = 64 with mixed routing on int8 V codes
+// (the 32-row kernel's split workgroups would need both V formats in LDS).
 //
 // Numerics follow attn_fwd (attention/triton/tilemix.py:503-951):
 //   qk_scale = fp32(sm_scale) * fp32(log2 e)                               (:641)
@@ -15,11 +17,10 @@
 //
 // Work decomposition (MI355X-first, not the reference's):
 //   * one workgroup = one (sequence, query head, block_m query rows);
-//     NW = block_m/16 waves, each wave owns 16 query rows.  A gfx950 wave
-//     issues about one instruction per 5 clocks and its MFMAs do not overlap
-//     its own VALU work, so throughput comes from co-issuing the MFMAs of one
-//     wave with the softmax of another: 16-row waves fit in 128 VGPRs, which
-//     gives 4 waves per SIMD (two workgroups per CU);
+//     NW = block_m/16 waves, each wave owns 16 query rows.  16-row waves fit
+//     in 128 VGPRs: 4 waves per SIMD at head_dim 64 (the MFMAs of one wave
+//     run beside the softmax of the others); at head_dim 128 the 64 KB of LDS
+//     per workgroup allows 2;
 //   * every wave computes S^T = K . Q^T with 16x16 MFMAs (16x16x32 f16,
 //     16x16x64 i8).  Lane l owns query row l%16 and keys 16 kb + 4 (l/16) + r
 //     (kb, r = 0..3) of each 64-key tile; a row's 4 lanes combine with one
@@ -47,8 +48,10 @@
 
 namespace tmx {
 
+// Occupancy target: 4 waves per SIMD at head_dim 64; at 128 the LDS allows 2.
 template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4, 4)))
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu(DP <= 64 ? 4 : 2, DP <= 64 ? 4 : 2)))
 attn16_kernel(const AttnKArgs a) {
   constexpr int BM = NW * 16;
   constexpr int KS16 = DP / 32;  // fp16 k-steps (16x16x32)
