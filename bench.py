@@ -180,13 +180,15 @@ def other_configs(device, steps: int):
     one tilemix_attention_with_quant step each, effective TOPS and the blended
     roofline fraction of the step.  cfg3: Qwen2-7B shape, B1 x 32768, Hq28/Hk4,
     D128, row_rand and bigbird at p = 0.5 (mask groups of 8 tiles).  cfg4: 24
-    packed sequences of 512..8192 tokens, Hq32/Hk8, align_sparse at p = 0.5."""
+    packed sequences of 512..8192 tokens, Hq32/Hk8, align_sparse at p = 0.5.
+    glue_L2048_block_m64 / _m128: the cfg2 heads at B8 x 2048 with SpTrans50,
+    at the block_m the model glue picks below 4096 tokens (64) and at 128."""
     import torch
     from tilemix_amd.attention import precision_maps as pm
     from tilemix_amd.attention.hip import tilemix as tmx
     from tilemix_amd.models._common import pick_mask_block_n
 
-    def run(lengths, hq, hk, pattern, bnm, seed, head_scale):
+    def run(lengths, hq, hk, pattern, bnm, seed, head_scale, block_m=128, pattern_params=None, warmup=3):
         g = torch.Generator(device=device)
         g.manual_seed(seed)
         n = sum(lengths)
@@ -200,24 +202,24 @@ def other_configs(device, steps: int):
         q, k, v = q.half(), k.half(), v.half()
         cu = torch.tensor([0] + list(itertools.accumulate(lengths)), dtype=torch.int32, device=device)
         lmax = max(lengths)
-        row = pm.make_precision_bitmask(lmax, 128, bnm, None, percentage=0.5, pattern_type=pattern,
-                                        pattern_params={}, COMPUTE_BLOCK_N=64)
+        row = pm.make_precision_bitmask(lmax, block_m, bnm, None, percentage=0.5, pattern_type=pattern,
+                                        pattern_params=pattern_params or {}, COMPUTE_BLOCK_N=64)
         bm = row.repeat(hk).to(device)
-        fn = lambda: tmx.tilemix_attention_with_quant(q, k, v, cu, cu, lmax, lmax, bm, block_m=128, block_n=64,
+        fn = lambda: tmx.tilemix_attention_with_quant(q, k, v, cu, cu, lmax, lmax, bm, block_m=block_m, block_n=64,
                                                       block_n_mask=bnm, BLKQ=128, BLKK=64, causal=True,
-                                                      int8_use_fp16_v=True)
-        ms = time_steps(fn, steps, 3)
+                                                      scalar_scales=(block_m == 128), int8_use_fp16_v=True)
+        ms = time_steps(fn, steps, warmup)
         ops = sum(algorithmic_ops(1, hq, D, ln) for ln in lengths)
         # INT8 fraction of the executed tiles, per sequence (row = hk * m_blocks(seq) + m)
         bits = [int(x) for x in row.tolist()] * hk
         total = routed = 0.0
         for ln in lengths:
-            mbz = (ln + 127) // 128
+            mbz = (ln + block_m - 1) // block_m
             nt = (ln + 63) // 64
             for h in range(hk):
                 for m in range(mbz):
                     raw = bits[h * mbz + m]
-                    for t in range(min(nt, ((m + 1) * 128 + 63) // 64)):
+                    for t in range(min(nt, ((m + 1) * block_m + 63) // 64)):
                         total += 1
                         routed += (raw >> (t // (bnm // 64))) & 1
         f = routed / total
@@ -233,6 +235,10 @@ def other_configs(device, steps: int):
     lengths = [int(x) for x in torch.randint(512, 8193, (24,), generator=rng)]
     out["cfg4_align_sparse50"] = run(lengths, 32, 8, "align_sparse", pick_mask_block_n(max(lengths), 64), 5, False)
     out["cfg4_align_sparse50"]["tokens"] = sum(lengths)
+    for bmv in (64, 128):
+        # ~0.3 ms steps: 200 warm-up steps bring the clocks up after the host-side map build
+        out[f"glue_L2048_block_m{bmv}"] = run([2048] * 8, HQ, HK, "sptrans", 64, 6, False, block_m=bmv,
+                                              pattern_params={"stride": 128, "c": 32}, warmup=200)
     return out
 
 
