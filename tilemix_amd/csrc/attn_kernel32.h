@@ -388,24 +388,33 @@ attn32_kernel(const AttnKArgs a) {
   if (n_blocks > 0) issue_next(0, smem_lds, route_next, sk_next, sv_next);
 
   const int half = SPLIT && wave >= NW / 2 ? 1 : 0;
-  for (int n = 0; n < n_blocks; ++n) {
+  // Start of tile n, for every wave: the tile has landed (own loads), then
+  // every wave's loads have landed and every wave is done with the other
+  // stage (tile n-1); then the next tile's copies go out.
+  auto tile_start = [&](int n) {
+    const int route = SPLIT ? (route_next >> half) & 1 : route_next;
+    __builtin_amdgcn_s_waitcnt(0);
+    if (INT8V && route == 1) widen_v8(smem + (n & 1) * STAGE);
+    __syncthreads();
+    if (n + 1 < n_blocks)
+      issue_next(n + 1, smem_lds + ((n + 1) & 1) * STAGE, route_next, sk_next, sv_next);
+  };
+  // Tiles [n_wave, n_blocks) are fully masked for this wave's rows (causal),
+  // or the wave's rows lie past the sequence end: the reference's update is
+  // then an exact no-op (p = 0, alpha = 1), so the wave only keeps the
+  // workgroup's barriers and copies going for them.  (A per-tile skip inside
+  // the compute loop made the register allocator copy the 64 accumulator
+  // VGPRs on every tile in some instantiations.)
+  int n_wave = n_blocks;
+  if (row0w >= Lq) n_wave = 0;
+  else if (a.causal) n_wave = min(n_blocks, row0w + 31 + diag < 0 ? 0 : (row0w + 31 + diag) / kBN + 1);
+  for (int n = 0; n < n_wave; ++n) {
     const int route = SPLIT ? (route_next >> half) & 1 : route_next;
     const f16 sk16 = sk_next;
     const f16 sv16 = sv_next;
     unsigned char* stage = smem + (n & 1) * STAGE;
-    // Tile n has landed (own loads), then every wave's loads have landed and
-    // every wave is done with the other stage (tile n-1).
-    __builtin_amdgcn_s_waitcnt(0);
-    if (INT8V && route == 1) widen_v8(stage);
-    __syncthreads();
-    if (n + 1 < n_blocks)
-      issue_next(n + 1, smem_lds + ((n + 1) & 1) * STAGE, route_next, sk_next, sv_next);
-
+    tile_start(n);
     const int key0 = n * kBN;
-    // Fully masked for this wave (or rows past the sequence end): the
-    // reference's update is then an exact no-op (p = 0, alpha = 1).
-    const bool wave_skip = (row0w >= Lq) || (a.causal && key0 > row0w + 31 + diag);
-    if (wave_skip) continue;
 
     // ---- S^T = K . Q^T, rounded to fp16 (packed pairs r, r+1) ----------
     uint32_t s16[2][8];
@@ -600,6 +609,7 @@ attn32_kernel(const AttnKArgs a) {
       }
     }
   }
+  for (int n = n_wave; n < n_blocks; ++n) tile_start(n);
 
   // ---- epilogue: out = fp16(acc / l) --------------------------------------
   {
