@@ -52,3 +52,46 @@ def test_reciprocal_division_equals_ieee_division():
         assert np.array_equal(code(q1), code(t_div)), f"amax={amax}"
         checked += x.size
     assert checked > 10_000_000
+
+
+def _rn32_exact(x):
+    """Round a Fraction to the nearest float32 (ties to even), normal range."""
+    from fractions import Fraction
+    if x == 0:
+        return Fraction(0)
+    sign = -1 if x < 0 else 1
+    x = abs(x)
+    e = x.numerator.bit_length() - x.denominator.bit_length()
+    if Fraction(2) ** e > x:
+        e -= 1
+    if Fraction(2) ** (e + 1) <= x:
+        e += 1
+    scale = Fraction(2) ** (23 - e)
+    m = x * scale
+    q, r = divmod(m.numerator, m.denominator)
+    if 2 * r > m.denominator or (2 * r == m.denominator and q & 1):
+        q += 1
+    return sign * Fraction(q) / scale
+
+
+def test_reciprocal_division_epilogue_domain():
+    """The attention epilogue computes acc / l the same way (r = RN(1/l), two
+    FMAs).  There the remainder is not always representable, so each FMA is
+    evaluated in exact rational arithmetic with one rounding to float32; on
+    random (acc, l) over the kernel's range (l in [1, 8192], |acc| in
+    [1e-6, 1e4]) the result equals the correctly rounded quotient."""
+    from fractions import Fraction
+    rng = np.random.default_rng(7)
+    n = 20000
+    ls = np.where(rng.random(n) < 0.3, rng.uniform(1.0, 2.0, n), rng.uniform(1.0, 8192.0, n)).astype(f32)
+    accs = (rng.choice([-1.0, 1.0], n) * 10.0 ** rng.uniform(-6, 4, n)).astype(f32)
+    inexact = 0
+    for a32, l32 in zip(accs, ls):
+        a, lv = Fraction(float(a32)), Fraction(float(l32))
+        r = _rn32_exact(1 / lv)
+        q0 = _rn32_exact(a * r)
+        rem = _rn32_exact(a - q0 * lv)
+        inexact += rem != a - q0 * lv
+        q1 = _rn32_exact(q0 + rem * r)
+        assert q1 == _rn32_exact(a / lv), (float(a32), float(l32))
+    assert inexact > 0  # the sample reaches the cases where the first FMA rounds

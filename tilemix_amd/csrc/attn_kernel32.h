@@ -125,93 +125,6 @@ attn32_kernel(const AttnKArgs a) {
   const int row = row0w + l32;            // this lane's query row
   const bool row_ok = row < Lq;
 
-  // ---- Q fragments (B operand of S^T = K . Q^T) --------------------------
-  // Lane (row, hi) holds Q[row][16 s + 8 hi .. + 7] for the fp16 k-steps s and
-  // Q8[row][32 s + 16 hi .. + 15] for the int8 k-steps.
-  f16x8 qf[KS16];
-  i32x4 q8f[KS8];
-  f16 sq16 = (f16)1.0f;
-  const bool q_fused = MODE != TILEMIX_ROUTING_FP16 && a.q_fused;
-  f16x8 qraw[KS16];
-  if (MODE != TILEMIX_ROUTING_INT8 || q_fused) {
-    const f16* qp = a.q + (int64_t)(q_start + row) * a.sq_t + (int64_t)h * a.sq_h;
-#pragma unroll
-    for (int s = 0; s < KS16; ++s) {
-      const int d0 = 16 * s + 8 * hi;
-      qraw[s] = (f16x8){};
-      if (row_ok && d0 < a.d) qraw[s] = *reinterpret_cast<const f16x8*>(qp + d0);
-    }
-  }
-  if (MODE != TILEMIX_ROUTING_INT8) {
-#pragma unroll
-    for (int s = 0; s < KS16; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) qf[s][e] = (f16)fp32_round((float)qraw[s][e] * a.qk_scale);
-  }
-  if (q_fused) {
-    // In-kernel Q quantisation (the workgroup's 128 rows are exactly one
-    // BLKQ = 128 block of this head): scale = max|q| / 127 over the block's
-    // rows inside the sequence, code = trunc(q / scale +- 0.5), the same
-    // arithmetic as quant_per_block_int8 with sm_scale = 1.
-    float am = 0.0f;
-#pragma unroll
-    for (int s = 0; s < KS16; ++s)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf((float)qraw[s][e]));
-    {
-      const float2 pr = swap_halves(am);
-      am = fmaxf(pr.x, pr.y);
-    }
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
-    if (lane == 0) q_red[wave] = am;
-    __syncthreads();
-    am = q_red[0];
-#pragma unroll
-    for (int w = 1; w < NW; ++w) am = fmaxf(am, q_red[w]);
-    const float qs = am / 127.0f;  // IEEE division
-    const float qr = 1.0f / qs;    // IEEE reciprocal (inf when qs == 0: codes are 0 then)
-    sq16 = (f16)qs;
-    // fp16 layout -> int8 layout: lanes l and l+32 exchange one half of each
-    // pair of fp16 k-steps (2 s, 2 s + 1), so each lane then holds
-    // Q[row][32 s + 16 hi .. + 15] as (x, y) = 8 + 8 consecutive values.
-#pragma unroll
-    for (int s = 0; s < KS8; ++s) {
-      u32x4 x = __builtin_bit_cast(u32x4, qraw[2 * s]);
-      u32x4 y = __builtin_bit_cast(u32x4, qraw[2 * s + 1]);
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const auto sw = __builtin_amdgcn_permlane32_swap(x[r], y[r], false, false);
-        x[r] = sw[0];
-        y[r] = sw[1];
-      }
-      const f16x8 xv = __builtin_bit_cast(f16x8, x), yv = __builtin_bit_cast(f16x8, y);
-      uint32_t w[4] = {0u, 0u, 0u, 0u};
-#pragma unroll
-      for (int e = 0; e < 16; ++e) {
-        float t = div_by_recip((float)(e < 8 ? xv[e] : yv[e - 8]), qs, qr);
-        t += (t >= 0.0f) ? 0.5f : -0.5f;
-        const int code = (qs == 0.0f) ? 0 : (int)t;
-        w[e >> 2] |= (uint32_t)(code & 0xff) << (8 * (e & 3));
-      }
-      q8f[s] = (i32x4){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
-    }
-  } else if (MODE != TILEMIX_ROUTING_FP16) {
-    const int8_t* qp = a.q8 + (int64_t)(q_start + row) * a.sq8_t + (int64_t)h * a.sq8_h;
-#pragma unroll
-    for (int s = 0; s < KS8; ++s) {
-      const int d0 = 32 * s + 16 * hi;
-      i32x4 raw = {};
-      if (row_ok && d0 < a.d) raw = *reinterpret_cast<const i32x4*>(qp + d0);
-      q8f[s] = raw;
-    }
-    const int qb = a.cu_qs[z], qe = a.cu_qs[z + 1];
-    if (qe > qb) {
-      const int idx = min(qb + row / a.blkq, qe - 1);
-      sq16 = a.sq[(int64_t)idx * a.hq + h];
-    }
-  }
-
   // ---- asynchronous tile loads (HBM -> LDS, no registers) -----------------
   // Each tile is fetched through raw buffers based at the tile's first key
   // and sized to the keys left in the sequence: rows past the end read as 0
@@ -358,6 +271,99 @@ attn32_kernel(const AttnKArgs a) {
     }
   };
 
+  // The first tile's copies go out before Q is loaded, so the two
+  // latencies overlap.
+  int route_next = 0;
+  f16 sk_next = (f16)1.0f, sv_next = (f16)1.0f;
+  if (n_blocks > 0) issue_next(0, smem_lds, route_next, sk_next, sv_next);
+
+  // ---- Q fragments (B operand of S^T = K . Q^T) --------------------------
+  // Lane (row, hi) holds Q[row][16 s + 8 hi .. + 7] for the fp16 k-steps s and
+  // Q8[row][32 s + 16 hi .. + 15] for the int8 k-steps.
+  f16x8 qf[KS16];
+  i32x4 q8f[KS8];
+  f16 sq16 = (f16)1.0f;
+  const bool q_fused = MODE != TILEMIX_ROUTING_FP16 && a.q_fused;
+  f16x8 qraw[KS16];
+  if (MODE != TILEMIX_ROUTING_INT8 || q_fused) {
+    const f16* qp = a.q + (int64_t)(q_start + row) * a.sq_t + (int64_t)h * a.sq_h;
+#pragma unroll
+    for (int s = 0; s < KS16; ++s) {
+      const int d0 = 16 * s + 8 * hi;
+      qraw[s] = (f16x8){};
+      if (row_ok && d0 < a.d) qraw[s] = *reinterpret_cast<const f16x8*>(qp + d0);
+    }
+  }
+  if (MODE != TILEMIX_ROUTING_INT8) {
+#pragma unroll
+    for (int s = 0; s < KS16; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) qf[s][e] = (f16)fp32_round((float)qraw[s][e] * a.qk_scale);
+  }
+  if (q_fused) {
+    // In-kernel Q quantisation (the workgroup's 128 rows are exactly one
+    // BLKQ = 128 block of this head): scale = max|q| / 127 over the block's
+    // rows inside the sequence, code = trunc(q / scale +- 0.5), the same
+    // arithmetic as quant_per_block_int8 with sm_scale = 1.
+    float am = 0.0f;
+#pragma unroll
+    for (int s = 0; s < KS16; ++s)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf((float)qraw[s][e]));
+    {
+      const float2 pr = swap_halves(am);
+      am = fmaxf(pr.x, pr.y);
+    }
+#pragma unroll
+    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    if (lane == 0) q_red[wave] = am;
+    __syncthreads();
+    am = q_red[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) am = fmaxf(am, q_red[w]);
+    const float qs = am / 127.0f;  // IEEE division
+    const float qr = 1.0f / qs;    // IEEE reciprocal (inf when qs == 0: codes are 0 then)
+    sq16 = (f16)qs;
+    // fp16 layout -> int8 layout: lanes l and l+32 exchange one half of each
+    // pair of fp16 k-steps (2 s, 2 s + 1), so each lane then holds
+    // Q[row][32 s + 16 hi .. + 15] as (x, y) = 8 + 8 consecutive values.
+#pragma unroll
+    for (int s = 0; s < KS8; ++s) {
+      u32x4 x = __builtin_bit_cast(u32x4, qraw[2 * s]);
+      u32x4 y = __builtin_bit_cast(u32x4, qraw[2 * s + 1]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const auto sw = __builtin_amdgcn_permlane32_swap(x[r], y[r], false, false);
+        x[r] = sw[0];
+        y[r] = sw[1];
+      }
+      const f16x8 xv = __builtin_bit_cast(f16x8, x), yv = __builtin_bit_cast(f16x8, y);
+      uint32_t w[4] = {0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 16; ++e) {
+        float t = div_by_recip((float)(e < 8 ? xv[e] : yv[e - 8]), qs, qr);
+        t += (t >= 0.0f) ? 0.5f : -0.5f;
+        const int code = (qs == 0.0f) ? 0 : (int)t;
+        w[e >> 2] |= (uint32_t)(code & 0xff) << (8 * (e & 3));
+      }
+      q8f[s] = (i32x4){(int)w[0], (int)w[1], (int)w[2], (int)w[3]};
+    }
+  } else if (MODE != TILEMIX_ROUTING_FP16) {
+    const int8_t* qp = a.q8 + (int64_t)(q_start + row) * a.sq8_t + (int64_t)h * a.sq8_h;
+#pragma unroll
+    for (int s = 0; s < KS8; ++s) {
+      const int d0 = 32 * s + 16 * hi;
+      i32x4 raw = {};
+      if (row_ok && d0 < a.d) raw = *reinterpret_cast<const i32x4*>(qp + d0);
+      q8f[s] = raw;
+    }
+    const int qb = a.cu_qs[z], qe = a.cu_qs[z + 1];
+    if (qe > qb) {
+      const int idx = min(qb + row / a.blkq, qe - 1);
+      sq16 = a.sq[(int64_t)idx * a.hq + h];
+    }
+  }
+
   // ---- online softmax state (one query row per lane) ----------------------
   // l_i is this lane's share of the row sum; both lanes of a row start at
   // 1.0 like the reference's l: the first tile with a valid key has
@@ -383,9 +389,6 @@ attn32_kernel(const AttnKArgs a) {
     if (MODE != TILEMIX_ROUTING_FP16 && kMagicC) asm volatile("" : "+v"(mv));
     magic_c[e] = mv;
   }
-  int route_next = 0;
-  f16 sk_next = (f16)1.0f, sv_next = (f16)1.0f;
-  if (n_blocks > 0) issue_next(0, smem_lds, route_next, sk_next, sv_next);
 
   const int half = SPLIT && wave >= NW / 2 ? 1 : 0;
   // Start of tile n, for every wave: the tile has landed (own loads), then
@@ -618,6 +621,13 @@ attn32_kernel(const AttnKArgs a) {
   }
   if (row_ok) {
     f16* op = a.out + (int64_t)(q_start + row) * a.so_t + (int64_t)h * a.so_h;
+    // acc / l from one IEEE reciprocal per row and Markstein's correction
+    // step per element (3 instructions instead of a full division each); the
+    // quotient is the correctly rounded one (checked against exact rational
+    // arithmetic on random pairs in tests/test_quant_division.py).  The
+    // barrier keeps it an fp32 value: folded into one mixed-precision FMA
+    // that rounds straight to fp16, it would differ on double-rounding ties.
+    const float rl = 1.0f / l_i;
 #pragma unroll
     for (int db = 0; db < NDB; ++db)
 #pragma unroll
@@ -626,7 +636,7 @@ attn32_kernel(const AttnKArgs a) {
         if (d0 < a.d) {
           f16x4 o;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) o[e] = (f16)(acc[db][4 * rq + e] / l_i);
+          for (int e = 0; e < 4; ++e) o[e] = (f16)fp32_round(div_by_recip(acc[db][4 * rq + e], l_i, rl));
           *reinterpret_cast<f16x4*>(op + d0) = o;
         }
       }
