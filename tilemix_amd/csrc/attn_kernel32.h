@@ -160,13 +160,20 @@ attn32_kernel(const AttnKArgs a) {
   const int step_v8 = NW * (1024 / ROW8) * (int)v8t_bytes;
   const uint32_t smem_lds = lds_addr(smem);
   // route: 0 fp16 / 1 int8; SPLIT: bit 0 the low half's route, bit 1 the high half's.
-  auto issue_tile = [&](int n, int route, uint32_t stage) {
-    const int key0 = n * kBN;
-    const int rem = Lk - key0;  // >= 1
+  // Base of the next tile in each stream and the bytes from there to the end
+  // of the sequence, advanced by one tile per issue (tiles are issued in
+  // order, one per call): no 64-bit multiplies in the loop.
+  const unsigned char* kcur = kseq;
+  const unsigned char* k8cur = k8seq;
+  const unsigned char* vcur = vseq;
+  const unsigned char* v8cur = v8seq;
+  int kleft = (int)(Lk * kt_bytes), k8left = (int)(Lk * k8t_bytes);
+  int vleft = (int)(Lk * vt_bytes), v8left = (int)(Lk * v8t_bytes);
+  auto issue_tile = [&](int route, uint32_t stage) {
     const bool need16 = MODE != TILEMIX_ROUTING_INT8 && (SPLIT ? route != 3 : route == 0);
     const bool need8 = MODE != TILEMIX_ROUTING_FP16 && route != 0;
     if (need16) {
-      const SRsrc rs = make_srsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
+      const SRsrc rs = make_srsrc(kcur, kleft);
       // Opaque copy of the lane offset: the per-copy sums are formed here, one
       // add each, instead of being hoisted into loop-invariant VGPRs (the
       // same for the LDS read bases below).
@@ -177,7 +184,7 @@ attn32_kernel(const AttnKArgs a) {
         async_load16_asm(rs, o + i * step_k16, stage + (i * NW + wave) * 1024);
     }
     if (need8) {
-      const SRsrc rs = make_srsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
+      const SRsrc rs = make_srsrc(k8cur, k8left);
       int o = dma_k8;
       asm volatile("" : "+v"(o));
 #pragma unroll
@@ -186,19 +193,31 @@ attn32_kernel(const AttnKArgs a) {
     }
     const uint32_t vstage = stage + KBUF;
     if (!INT8V || route == 0) {
-      const SRsrc rs = make_srsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
+      const SRsrc rs = make_srsrc(vcur, vleft);
       int o = dma_v16;
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < V16_INS; ++i)
         async_load16_asm(rs, o + i * step_v16, vstage + (i * NW + wave) * 1024);
     } else {
-      const SRsrc rs = make_srsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
+      const SRsrc rs = make_srsrc(v8cur, v8left);
       int o = dma_v8;
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < V8_INS; ++i)
         async_load16_asm(rs, o + i * step_v8, stage + V8OFF + (i * NW + wave) * 1024);
+    }
+    kcur += kBN * kt_bytes;
+    kleft -= kBN * (int)kt_bytes;
+    vcur += kBN * vt_bytes;
+    vleft -= kBN * (int)vt_bytes;
+    if (MODE != TILEMIX_ROUTING_FP16) {
+      k8cur += kBN * k8t_bytes;
+      k8left -= kBN * (int)k8t_bytes;
+    }
+    if (INT8V) {
+      v8cur += kBN * v8t_bytes;
+      v8left -= kBN * (int)v8t_bytes;
     }
   };
 
@@ -228,15 +247,22 @@ attn32_kernel(const AttnKArgs a) {
   // divisions in the loop): tile t has route group t / mask_tiles and scale
   // block key0 / blkk = t / (blkk / 64).
   const int kb_tiles = a.blkk / kBN;
-  int nx_grp = 0, nx_gc = 0, nx_sb = 0, nx_sc = 0;  // of the next tile to issue
-  int kbase = 0, kend = 0, vbase = 0, vend = 0;
+  int nx_grp = 0, nx_gc = 0, nx_sc = 0;  // of the next tile to issue
+  // Scale of the next tile's block (clamped at the sequence's last block, the
+  // reference's min(block, last) lookup), advanced by pointer.
+  bool has_ks = false, has_vs = false;
+  const f16 *skp = nullptr, *sk_last = nullptr, *svp = nullptr, *sv_last = nullptr;
   if (MODE != TILEMIX_ROUTING_FP16) {
-    kbase = a.cu_ks[z];
-    kend = a.cu_ks[z + 1];
+    const int kbase = a.cu_ks[z], kend = a.cu_ks[z + 1];
+    has_ks = kend > kbase;
+    skp = a.sk + (int64_t)kbase * a.hk + hk;
+    sk_last = a.sk + (int64_t)(kend - 1) * a.hk + hk;
   }
   if (INT8V) {
-    vbase = a.cu_vs[z];
-    vend = a.cu_vs[z + 1];
+    const int vbase = a.cu_vs[z], vend = a.cu_vs[z + 1];
+    has_vs = vend > vbase;
+    svp = a.sv + (int64_t)vbase * a.hk + hk;
+    sv_last = a.sv + (int64_t)(vend - 1) * a.hk + hk;
   }
   // Issues the next tile (index nx) and fetches its scales; the loads land
   // before the barrier that precedes the tile's compute.
@@ -252,14 +278,10 @@ attn32_kernel(const AttnKArgs a) {
       const int rlo = nx * kBN > lo_last_key ? rhi : (int)((bits >> (unsigned)nx_grp) & 1ull);
       route = rlo | (rhi << 1);
     }
-    issue_tile(nx, route, stage);
+    issue_tile(route, stage);
     if (MODE != TILEMIX_ROUTING_FP16 && route != 0) {
-      skv = (f16)1.0f;
-      if (kend > kbase) skv = a.sk[(int64_t)min(kbase + nx_sb, kend - 1) * a.hk + hk];
-      if (INT8V) {
-        svv = (f16)1.0f;
-        if (vend > vbase) svv = a.sv[(int64_t)min(vbase + nx_sb, vend - 1) * a.hk + hk];
-      }
+      skv = has_ks ? *skp : (f16)1.0f;
+      if (INT8V) svv = has_vs ? *svp : (f16)1.0f;
     }
     if (++nx_gc == a.mask_tiles) {
       nx_gc = 0;
@@ -267,7 +289,8 @@ attn32_kernel(const AttnKArgs a) {
     }
     if (++nx_sc == kb_tiles) {
       nx_sc = 0;
-      ++nx_sb;
+      if (MODE != TILEMIX_ROUTING_FP16 && skp != sk_last) skp += a.hk;
+      if (INT8V && svp != sv_last) svp += a.hk;
     }
   };
 
