@@ -368,3 +368,27 @@ def test_separate_q_and_k_lengths(device, block_m):
                      q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
                      cu_q_scale=cq, cu_k_scale=ck)
     assert_close_out(out.cpu().numpy(), ref)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_random_configurations(device, seed):
+    """Seeded random draws over the launch space (1-4 sequences of 1..700
+    tokens, GQA groups, head_dim 64/80/128, block_m 64/128, mask groups of 1
+    or 2 tiles, causal or not, mixed/fp16/int8 routing, fp16 or int8 V) against
+    the oracle at the full bar.  Covers the kernel selection (32-row, split
+    32-row, 16-row) and the wave-tail loop with shapes no fixed case lists."""
+    rng = np.random.default_rng(1000 + seed)
+    n_seq = int(rng.integers(1, 5))
+    lengths = [int(x) for x in rng.integers(1, 701, n_seq)]
+    hq, hk = [(4, 1), (4, 2), (6, 2), (8, 8), (6, 3)][int(rng.integers(0, 5))]
+    d = [64, 80, 128][int(rng.integers(0, 3))]
+    block_m = [64, 128][int(rng.integers(0, 2))]
+    bnm = [64, 128][int(rng.integers(0, 2))]
+    causal = bool(rng.integers(0, 4))  # 3 in 4 causal
+    mode = ["mixed", "mixed", "fp16", "int8"][int(rng.integers(0, 4))]
+    int8v = True if mode == "fp16" else bool(rng.integers(0, 2))  # int8_use_fp16_v
+    print(f"seed {seed}: lengths {lengths} hq {hq} hk {hk} d {d} block_m {block_m} bnm {bnm} "
+          f"causal {causal} mode {mode} int8_use_fp16_v {int8v}", flush=True)
+    got, ref, _ = _run_case(device, lengths, hq, hk, d, block_m, bnm, causal, mode, int8v, "rand",
+                            seed=2000 + seed)
+    assert_close_out(got, ref)
