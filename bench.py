@@ -16,7 +16,12 @@ times the CPU oracle (numpy fp32 emulation) on a bounded slice of the same
 workload on this host; ``extra.e2e_prefill_ms`` is BASELINE configs[4] (random-
 init fp16 Llama-3.2-3B prefill, B=8 x 4096, TileMix SpTrans50 in every layer).
 
-    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-e2e] [--sweep]
+The default run also reports, in ``extra``: the SpTrans p-sweep
+{0, .25, .5, .75, 1} (kernel and step), BASELINE configs 3 and 4 and the
+model glue's B8 x 2048 shapes (one step each), and BASELINE configs[0] (cfg1)
+on the GPU beside the CPU oracle's median of 20 runs.
+
+    python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-e2e] [--no-sweep]
 """
 from __future__ import annotations
 
@@ -242,6 +247,69 @@ def other_configs(device, steps: int):
     return out
 
 
+def host_cpu() -> dict:
+    """CPU model and thread counts of this host (reported with the CPU baseline)."""
+    import torch
+    model = platform.processor() or platform.machine()
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count(), "torch_num_threads": torch.get_num_threads()}
+
+
+def cfg1(device, runs: int = 20, warmup: int = 5, with_cpu: bool = True):
+    """B1, Hq4/Hk1, D64, L256, causal, band p=0.5, 64x64
+    tiles, fp16 N(0,1) from seed 0, through tilemix_varlen_attention.  GPU:
+    mean step ms over `runs` steps; CPU: the oracle (numpy fp32 emulation incl.
+    quantisation) on the same inputs, median ms of `runs` runs after 1 warmup."""
+    import numpy as np
+    import torch
+    from oracle import tilemix_oracle as O
+    from tilemix_amd.attention import precision_maps as pm
+    from tilemix_amd.attention.tilemix_varlen import tilemix_varlen_attention
+
+    g = torch.Generator().manual_seed(0)
+    b, hq, hk, t, d = 1, 4, 1, 256, 64
+    q = torch.randn(b, hq, t, d, generator=g).half()
+    k = torch.randn(b, hk, t, d, generator=g).half()
+    v = torch.randn(b, hk, t, d, generator=g).half()
+    row = pm.make_precision_bitmask(t, 64, 64, None, percentage=0.5, pattern_type="band", pattern_params={},
+                                    COMPUTE_BLOCK_N=64)
+    pmap = row.repeat(hk).to(device)
+    qd, kd, vd = q.to(device), k.to(device), v.to(device)
+    fn = lambda: tilemix_varlen_attention(qd, kd, vd, 64, 64, block_n_mask=64, causal=True, scale=d ** -0.5,
+                                          precision_map_all=pmap, candidates=[(64, 64)],
+                                          flat_lengths=[pmap.numel()])
+    gpu_ms = time_steps(fn, runs, warmup)
+    out = {"gpu_step_ms": gpu_ms, "eff_tops": algorithmic_ops(1, hq, d, t) / (gpu_ms * 1e-3) / 1e12}
+    if with_cpu:
+        qn = q.permute(0, 2, 1, 3).reshape(t, hq, d).numpy()
+        kn = k.permute(0, 2, 1, 3).reshape(t, hk, d).numpy()
+        vn = v.permute(0, 2, 1, 3).reshape(t, hk, d).numpy()
+        cu = np.array([0, t])
+        bits = np.array([int(x) for x in pmap.cpu().tolist()], dtype=np.uint64)
+
+        def oracle():
+            q8, sq, cuq = O.quant_per_block_int8(qn, cu, 128)
+            k8, sk, cuk = O.quant_per_block_int8(kn, cu, 64)
+            return O.attn_fwd(qn, kn, vn, cu, cu, bits, block_m=64, block_n_mask=64, causal=True, q8=q8, k8=k8,
+                              sq16=sq.astype(np.float16), sk16=sk.astype(np.float16), cu_q_scale=cuq,
+                              cu_k_scale=cuk)
+        oracle()
+        times = []
+        for _ in range(runs):
+            t0 = time.perf_counter()
+            oracle()
+            times.append((time.perf_counter() - t0) * 1e3)
+        out["cpu_oracle_median_ms"] = statistics.median(times)
+        out["cpu_note"] = f"median of {runs} runs after 1 warmup, numpy oracle on this host's CPU"
+    return out
+
+
 def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 4):
     """Oracle (numpy fp32 emulation) on sequence 0, the first `sample_groups`
     KV groups (3 query heads each), quantisation included; scaled to TOPS."""
@@ -263,6 +331,7 @@ def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 4):
     secs = time.perf_counter() - t0
     ops = algorithmic_ops(b=1, hq=hq)
     threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+    host = host_cpu()
     return {
         "value": ops / secs / 1e12,
         "unit": "TOPS",
@@ -270,9 +339,10 @@ def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 4):
         "kind": "port",
         "sample": (f"numpy oracle (fp32 emulation incl. int8 quantisation), sequence 0, "
                    f"{hq} query heads / {sample_groups} KV heads of the B8 L4096 SpTrans50 workload; "
-                   f"{secs:.2f} s for {ops:.3e} ops; host {platform.processor() or platform.machine()}, "
-                   f"os.cpu_count()={os.cpu_count()}"),
+                   f"{secs:.2f} s for {ops:.3e} ops; BLAS threads {threads}; host {host['cpu_model']}, "
+                   f"os.cpu_count()={host['os_cpu_count']}, torch.get_num_threads()={host['torch_num_threads']}"),
         "seconds": secs,
+        **host,
     }
 
 
@@ -283,7 +353,8 @@ def main() -> int:
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-e2e", action="store_true", help="skip the e2e Llama-3.2-3B prefill timing")
-    ap.add_argument("--sweep", action="store_true", help="also time SpTrans p in {0,.25,.5,.75,1}")
+    ap.add_argument("--no-sweep", action="store_true",
+                    help="skip the SpTrans p-sweep, configs 1/3/4 and the glue shapes")
     ap.add_argument("--kernel-only", type=int, default=0, metavar="N",
                     help="profiling mode: launch only the SpTrans50 attention kernel N times, print nothing else")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
@@ -376,7 +447,7 @@ def main() -> int:
     ms_fp16map = time_steps(step_fn(bm0), args.steps, 2)
 
     sweep = None
-    if args.sweep:
+    if not args.no_sweep:
         sweep = {}
         for p in (0.0, 0.25, 0.5, 0.75, 1.0):
             row, bmp = sptrans_map(p, device)
@@ -387,8 +458,9 @@ def main() -> int:
                              "kernel_roofline_frac": roofline_seconds(fp, ops) / (kp * 1e-3)}
 
     others = None
-    if args.sweep:
+    if not args.no_sweep:
         others = other_configs(device, args.steps)
+        others["cfg1_band50"] = cfg1(device, with_cpu=not args.no_cpu)
 
     e2e_ms = None
     if not args.no_e2e:

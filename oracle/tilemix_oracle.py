@@ -161,19 +161,61 @@ def _scale_rows(scale16: np.ndarray, base: int, end: int, idx: np.ndarray, head:
     return scale16[j, head].astype(f16)
 
 
+def fp16_tile_scores(q16: np.ndarray, k16: np.ndarray, accum: str = "exact") -> np.ndarray:
+    """FP16 route scores fp16(dot(q16, k)) of attention/triton/tilemix.py:254, [Lq, Lk].
+
+    The reference asks Triton for ``out_dtype=float16``; how its dot accumulates
+    is the compiler's and the GPU's (unpinned: no reference output pins it).
+    Three models of the sum over head_dim before the final fp16 rounding:
+
+    * ``"exact"``: the exact sum, rounded once (the oracle's definition);
+    * ``"fp32_k16"``: an fp32 accumulator updated once per 16-wide slice of
+      head_dim in ascending order, each update the exact slice sum added with
+      one fp32 rounding (the k-step order of the 32x32x16 f16 MFMA; the
+      MFMA's internal summation of a k-step rounds differently, its fp32
+      accumulators differ from this model by a few ulps on most entries, so
+      this is a model of fp32 accumulation, not of the instruction's bits);
+    * ``"fp16_k16"``: the same with an fp16 accumulator (a model of an
+      fp16-accumulating matrix instruction per 16-wide slice).
+
+    Products of two fp16 values are exact in fp64 and a 16-term slice sum is
+    exact in fp64 unless its terms span more than ~27 binary orders of
+    magnitude, which these inputs never reach.
+    """
+    if accum == "exact":
+        return (q16.astype(np.float64) @ k16.astype(np.float64).T).astype(f16)
+    if accum not in ("fp32_k16", "fp16_k16"):
+        raise ValueError(f"unknown accumulation model {accum!r}")
+    return k16_accumulate(q16, k16, f32 if accum == "fp32_k16" else f16).astype(f16)
+
+
+def k16_accumulate(q16: np.ndarray, k16: np.ndarray, acc_dtype=f32) -> np.ndarray:
+    """The accumulator of dot(q16, k16^T) updated once per 16-wide slice of
+    head_dim (ascending), each update = exact slice sum added with one rounding
+    to ``acc_dtype``; returned unrounded to fp16 ([Lq, Lk] of acc_dtype)."""
+    qd = q16.astype(np.float64)
+    kd = k16.astype(np.float64)
+    acc = np.zeros((q16.shape[0], k16.shape[0]), dtype=acc_dtype)
+    for d0 in range(0, q16.shape[1], 16):
+        part = qd[:, d0:d0 + 16] @ kd[:, d0:d0 + 16].T
+        acc = (acc.astype(np.float64) + part).astype(acc_dtype)
+    return acc
+
+
 def attn_fwd(q, k, v, cu_q, cu_k, bitmask, *, block_m: int, block_n_mask: int, causal: bool,
              sm_scale: float | None = None, routing_mode: int = ROUTING_MIXED,
              q8=None, k8=None, sq16=None, sk16=None, cu_q_scale=None, cu_k_scale=None,
              blkq: int = 128, blkk: int = 64, int8_use_fp16_v: bool = True,
              v8=None, sv16=None, cu_v_scale=None, bias=None, want_scores: bool = False,
-             qk16_override=None):
+             qk16_override=None, fp16_accum: str = "exact"):
     """fp32 emulation of attn_fwd over packed varlen [tokens, heads, dim] fp16 input.
 
     Returns out (float16, shape of q); with want_scores also a dict mapping
     (z, h) -> (qk_i32 [Lq, Lk] int64 (exact), qk16 [Lq, Lk] float16 pre-mask
     scores, route [Lq, Lk] bool).  ``qk16_override`` (callable (z, h) -> fp16
     [Lq, Lk] or None) replaces the score stage, so the softmax/PV stage can be
-    checked on given scores.
+    checked on given scores.  ``fp16_accum`` is the accumulation of the FP16
+    route's dot(q16, k) before its fp16 rounding (see ``fp16_tile_scores``).
     """
     q = np.asarray(q)
     k = np.asarray(k)
@@ -212,7 +254,7 @@ def attn_fwd(q, k, v, cu_q, cu_k, bitmask, *, block_m: int, block_n_mask: int, c
             acc_i32 = None
             if not route.all():
                 q16s = (qh * qk_scale).astype(f16)                           # :643-649
-                s16 = (q16s.astype(np.float64) @ kh.T.astype(np.float64)).astype(f16)  # :254
+                s16 = fp16_tile_scores(q16s, kh.astype(f16), fp16_accum)      # :254
                 qk16 = np.where(route, qk16, s16)
             if need_int8 and route.any():
                 q8h = np.asarray(q8)[qs:qs + Lq, h].astype(np.float64)

@@ -1,0 +1,165 @@
+"""Host-side model of the attention kernels' HBM->LDS tile copies: which bytes a
+launch reads.
+
+The kernels copy every 64-key tile of K (fp16 or int8), V (fp16) and int8 V
+codes with ``buffer_load_dwordx4 ... lds`` through a raw buffer based at the
+tile's first key (sequence start + head offset) whose size is the bytes left
+to the sequence end; a 4-byte lane of the load reads memory only below that
+size (zeros otherwise).  The lane offsets restated here are those of
+``lane_off0`` / ``issue_tile`` in tilemix_amd/csrc/attn_kernel32.h and of
+``lane_off`` / ``issue_tile`` in tilemix_amd/csrc/attn_kernel16.h (swizzles:
+``swz_k``, ``swz_v``, ``swz_v32`` in attn_common.h; out-of-range offset
+``kOffOutside``).
+
+The check: every byte read is a byte of an element (token of the tile's own
+sequence, the tile's KV head, column < head_dim) -- nothing past the end of a
+tensor, nothing of a neighbouring head, nothing of the padded columns.  With
+the head_dim mask taken out (the copies before the fix), the model reads past
+the end of the last head of the last token, which the planted case asserts.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+OUTSIDE = 0x80000000  # kOffOutside as a 32-bit lane offset
+
+
+def swz_k(rowb, r):
+    if rowb >= 256:
+        return r & 15
+    if rowb == 128:
+        return (r >> 1) & 7
+    return (r >> 2) & 3
+
+
+def swz_v(rowb, r):
+    return 2 * (r & 7) if rowb >= 256 else 2 * ((r >> 1) & 3)
+
+
+def swz_v32(rowb, r):
+    return 4 * (r & 3) if rowb >= 256 else 4 * ((r >> 1) & 1)
+
+
+def lane_offsets(kernel, rowb, tok_bytes, swz, valid_bytes, nw=4, mask=True):
+    """u32 lane offsets of one tile's copies of one stream (all waves, lanes, copies)."""
+    rpi, cpr = 1024 // rowb, rowb // 16
+    offs = []
+    if kernel == 32:
+        ins = 64 * rowb // 1024 // nw
+        step = nw * rpi * tok_bytes
+        for wave in range(nw):
+            for lane in range(64):
+                r = wave * rpi + lane // cpr
+                chunk = (lane % cpr) ^ swz(rowb, r)
+                o0 = OUTSIDE if (mask and chunk * 16 >= valid_bytes) else r * tok_bytes + chunk * 16
+                for i in range(ins):
+                    offs.append((o0 + i * step) & 0xFFFFFFFF)
+    else:
+        tiles = 64 * rowb // 1024
+        n_i = (tiles + nw - 1) // nw
+        for i in range(n_i):
+            for wave in range(nw):
+                L = i * nw + wave
+                if L >= tiles:
+                    continue
+                for lane in range(64):
+                    r = L * rpi + lane // cpr
+                    chunk = (lane % cpr) ^ swz(rowb, r)
+                    o = OUTSIDE if (mask and chunk * 16 >= valid_bytes) else r * tok_bytes + chunk * 16
+                    offs.append(o & 0xFFFFFFFF)
+    return np.array(offs, dtype=np.int64)
+
+
+def bytes_read(offs, lens, hk, tok_bytes, head_bytes):
+    """Relative byte addresses (from the tensor's data pointer) read by the copies."""
+    out = []
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    dw = offs[:, None] + 4 * np.arange(4)[None, :]  # every dword of every lane
+    for z, L in enumerate(lens):
+        for h in range(hk):
+            for t in range((L + 63) // 64):
+                base = (cu[z] + 64 * t) * tok_bytes + h * head_bytes
+                size = (L - 64 * t) * tok_bytes
+                hit = dw[dw < size]
+                out.append((base + hit[:, None] + np.arange(4)[None, :]).ravel())
+    return np.concatenate(out) if out else np.zeros(0, dtype=np.int64)
+
+
+def check_elements(addr, lens, hk, tok_bytes, head_bytes, elem, d):
+    """Every byte address lies in a valid element: token < total, head < hk, column < d."""
+    n = int(sum(lens))
+    assert addr.min() >= 0
+    tok, within = addr // tok_bytes, addr % tok_bytes
+    head, col = within // head_bytes, (within % head_bytes) // elem
+    bad = (tok >= n) | (head >= hk) | (col >= d)
+    return int(bad.sum())
+
+
+# kernel, head_dim, padded width DP, Hk, storage width (head stride in elements), lengths
+CASES = [
+    (32, 80, 128, 3, 80, [1, 63, 64, 65, 130]),
+    (32, 80, 128, 3, 128, [200, 7]),  # [..., :80] view of a 128-wide buffer
+    (32, 96, 128, 2, 96, [129, 64]),
+    (32, 112, 128, 2, 112, [70]),
+    (32, 48, 64, 3, 48, [100, 1]),
+    (32, 16, 64, 2, 16, [65]),
+    (32, 128, 128, 3, 128, [130]),
+    (16, 80, 128, 3, 80, [1, 63, 64, 65, 130]),
+    (16, 48, 64, 3, 48, [100, 1]),
+    (16, 32, 64, 2, 32, [64, 3]),
+]
+
+
+def _streams(kernel, dp, d, hstride, hk):
+    """(rowb, tok_bytes, head_bytes, elem bytes, valid bytes, swizzle) per copy stream."""
+    row16, row8 = 2 * dp, dp
+    tok16, tok8 = 2 * hstride * hk, hstride * hk
+    # int8 tensors need 16-byte strides: round the int8 head stride up
+    h8 = ((hstride + 15) // 16) * 16
+    tok8 = h8 * hk
+    vswz = swz_v32 if kernel == 32 else swz_v
+    return [
+        ("k16", row16, tok16, 2 * hstride, 2, 2 * d, swz_k),
+        ("v16", row16, tok16, 2 * hstride, 2, 2 * d, vswz),
+        ("k8", row8, tok8, h8, 1, d, swz_k),
+        ("v8", row8, tok8, h8, 1, d, swz_k),
+    ]
+
+
+@pytest.mark.parametrize("kernel,d,dp,hk,hstride,lens", CASES)
+def test_copies_read_only_valid_elements(kernel, d, dp, hk, hstride, lens):
+    for name, rowb, tok, head, elem, valid, swz in _streams(kernel, dp, d, hstride, hk):
+        offs = lane_offsets(kernel, rowb, tok, swz, valid)
+        addr = bytes_read(offs, lens, hk, tok, head)
+        assert addr.size > 0
+        bad = check_elements(addr, lens, hk, tok, head, elem, d)
+        assert bad == 0, f"{name}: {bad} bytes outside the valid elements"
+
+
+@pytest.mark.parametrize("kernel", [32, 16])
+def test_planted_unmasked_copy_reads_past_the_end(kernel):
+    """Without the head_dim mask, d=80 in a dense [N, 3, 80] K reads past the
+    tensor's end (last head, last token) and into the neighbouring head."""
+    d, dp, hk, lens = 80, 128, 3, [1, 63, 64, 65, 130]
+    name, rowb, tok, head, elem, valid, swz = _streams(kernel, dp, d, d, hk)[0]
+    offs = lane_offsets(kernel, rowb, tok, swz, valid, mask=False)
+    addr = bytes_read(offs, lens, hk, tok, head)
+    n_bytes = sum(lens) * tok
+    assert addr.max() >= n_bytes  # past the end of the allocation
+    assert check_elements(addr, lens, hk, tok, head, elem, d) > 0
+
+
+def test_lds_receives_every_valid_chunk_once():
+    """The copies of one tile fill each (row, column chunk < head_dim) exactly
+    once: the mask removes only padded columns (32-row kernel, K fp16, d=80)."""
+    d, dp, hk = 80, 128, 1
+    rowb, tok = 2 * dp, 2 * d
+    rpi, cpr, nw = 1024 // rowb, rowb // 16, 4
+    seen = np.zeros((64, cpr), dtype=np.int64)
+    for o in lane_offsets(32, rowb, tok, swz_k, 2 * d):
+        if o >= OUTSIDE:
+            continue
+        seen[o // tok, (o % tok) // 16] += 1
+    assert (seen[:, : 2 * d // 16] == 1).all()
+    assert (seen[:, 2 * d // 16:] == 0).all()

@@ -19,31 +19,13 @@ import pytest
 import torch
 
 from oracle import tilemix_oracle as O
+from tests._fullsize import (BM, CFG2_BLOCKS, CFG2_EXACT_MAX_ABS, CFG2_OUTLIERS, _inputs, _oracle_block,
+                             _row_map)
 from tests._helpers import assert_close_out, bitmask_tensor, to_dev
-from tilemix_amd.attention import precision_maps as pm
 from tilemix_amd.attention.hip import tilemix as tmx
 from tilemix_amd.models._common import pick_mask_block_n
 
 pytestmark = pytest.mark.gpu
-
-BM = 128
-
-
-def _inputs(lengths, hq, hk, d, seed, head_scale=False, outliers=()):
-    rng = np.random.default_rng(seed)
-    n = int(sum(lengths))
-    q = rng.standard_normal((n, hq, d), dtype=np.float32)
-    k = rng.standard_normal((n, hk, d), dtype=np.float32)
-    v = rng.standard_normal((n, hk, d), dtype=np.float32)
-    if head_scale:  # per-head scale ~ U(0.5, 2)
-        q *= rng.uniform(0.5, 2.0, size=(1, hq, 1)).astype(np.float32)
-        k *= rng.uniform(0.5, 2.0, size=(1, hk, 1)).astype(np.float32)
-        v *= rng.uniform(0.5, 2.0, size=(1, hk, 1)).astype(np.float32)
-    for c in outliers:
-        q[:, :, c] *= 8.0
-        k[:, :, c] *= 8.0
-    cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int32)
-    return q.astype(np.float16), k.astype(np.float16), v.astype(np.float16), cu
 
 
 def _launch(q, k, v, cu, bits, bnm, device):
@@ -57,58 +39,122 @@ def _launch(q, k, v, cu, bits, bnm, device):
     return out.cpu().numpy()
 
 
-def _oracle_block(q, k, v, cu, bits, hk, z, m, bnm):
-    """Oracle output of query block m of sequence z (Lq == Lk per sequence)."""
-    s0, L = int(cu[z]), int(cu[z + 1] - cu[z])
-    rows = min(BM, L - m * BM)
-    kend = m * BM + rows
-    qs = q[s0 + m * BM:s0 + m * BM + rows]
-    ks, vs = k[s0:s0 + kend], v[s0:s0 + kend]
-    cuq = np.array([0, rows], dtype=np.int32)
-    cuk = np.array([0, kend], dtype=np.int32)
-    mbz = -(-L // BM)
-    sub_bits = np.array([int(bits[h * mbz + m]) for h in range(hk)], dtype=np.uint64)
-    q8, sq, cuqs = O.quant_per_block_int8(qs, cuq, 128)
-    k8, sk, cuks = O.quant_per_block_int8(ks, cuk, 64)
-    return O.attn_fwd(qs, ks, vs, cuq, cuk, sub_bits, block_m=BM, block_n_mask=bnm, causal=True,
-                      routing_mode=O.ROUTING_MIXED, q8=q8, k8=k8, sq16=sq.astype(np.float16),
-                      sk16=sk.astype(np.float16), cu_q_scale=cuqs, cu_k_scale=cuks)
-
-
-def _row_map(L, bnm, pattern, params, hk):
-    row = pm.make_precision_bitmask(L, BM, bnm, None, percentage=0.5, pattern_type=pattern,
-                                    pattern_params=params, COMPUTE_BLOCK_N=64)
-    return np.array([int(x) for x in row.tolist()] * hk, dtype=np.uint64)
-
-
-def test_cfg2_full_size_blocks(device):
-    """B8 x 4096, Hq24/Hk8, D128, SpTrans50, 4 outlier channels x8 (the bench workload's shape)."""
+@pytest.fixture(scope="module")
+def cfg2(device):
+    """B8 x 4096, Hq24/Hk8, D128, SpTrans50, 4 outlier channels x8 (the bench workload)."""
     lengths, hq, hk = [4096] * 8, 24, 8
-    q, k, v, cu = _inputs(lengths, hq, hk, 128, seed=2, outliers=(7, 33, 70, 101))
+    q, k, v, cu = _inputs(lengths, hq, hk, 128, seed=2, outliers=CFG2_OUTLIERS)
     bits = _row_map(4096, 64, "sptrans", {"stride": 128, "c": 32}, hk)
     out = _launch(q, k, v, cu, bits, 64, device)
+    return dict(q=q, k=k, v=v, cu=cu, bits=bits, out=out, hq=hq, hk=hk)
+
+
+def _report(tag, d):
+    print(f"{tag}: max-abs {d.max():.3e} mean-abs {d.mean():.3e} within 2e-3 {(d <= 2e-3).mean():.6f}",
+          flush=True)
+
+
+def test_cfg2_full_size_blocks(cfg2):
+    """Full cfg2 launch, block by block.  Against the oracle whose FP16-route
+    scores sum in fp32 in the MFMA's k-step order (fp32 accumulator per 16-wide
+    k-step): the strict bar, max-abs 2e-3 / mean-abs 2e-4.  Against the exact-sum oracle:
+    mean-abs 2e-4, 99.9% of elements within 2e-3 and max-abs below
+    CFG2_EXACT_MAX_ABS -- on these x8-outlier inputs the softmax is peaked and a
+    one-ulp move of an fp16 score (fp32 vs exact accumulation) moves an output
+    by up to ~2e-2, as the CPU comparison of the two oracles shows without any
+    kernel."""
+    q, k, v, cu, bits, out, hk = (cfg2[x] for x in ("q", "k", "v", "cu", "bits", "out", "hk"))
     assert np.isfinite(out).all()
-    for z, m in ((0, 0), (0, 17), (3, 31), (7, 31)):
-        ref = _oracle_block(q, k, v, cu, bits, hk, z, m, 64)
+    for z, m in CFG2_BLOCKS:
         s = int(cu[z]) + m * BM
-        got = out[s:s + ref.shape[0]]
+        ref32 = _oracle_block(q, k, v, cu, bits, hk, z, m, 64, fp16_accum="fp32_k16")
+        got = out[s:s + ref32.shape[0]]
+        d32 = np.abs(got.astype(np.float64) - ref32.astype(np.float64))
+        _report(f"cfg2 block ({z},{m}) vs fp32-k16 oracle", d32)
+        assert d32.max() <= 2e-3 and d32.mean() <= 2e-4, (z, m, d32.max(), d32.mean())
+        ref = _oracle_block(q, k, v, cu, bits, hk, z, m, 64)
         d = np.abs(got.astype(np.float64) - ref.astype(np.float64))
-        # peaked softmax (x8 outlier channels): a 1-ulp FP16-score flip moves an
-        # output by up to ~1e-2; the bulk stays within the strict bar
-        assert d.mean() <= 2e-4 and (d <= 2e-3).mean() >= 0.999, (z, m, d.max(), d.mean())
+        _report(f"cfg2 block ({z},{m}) vs exact oracle", d)
+        assert d.mean() <= 2e-4 and (d <= 2e-3).mean() >= 0.999 and d.max() <= CFG2_EXACT_MAX_ABS, (z, m)
 
 
-def test_cfg3_full_size_blocks(device):
-    """B1 x 32768, Hq28/Hk4 (Qwen2-7B), D128, per-head scales, row_rand 0.5, mask groups of 8."""
+@pytest.mark.parametrize("z,m", [(0, 31), (3, 17)])
+def test_cfg2_decomposed_strict(device, cfg2, z, m):
+    """The query block (z, m) of cfg2 run as its own sub-problem (128 rows over
+    the keys up to its last row) through the kernel's dump instantiation:
+    * its output equals the full launch's rows bit for bit;
+    * the INT8-route scores and int32 accumulators equal the oracle's;
+    * the FP16-route fp16 scores (fp32 MFMA accumulation, rounded once) are
+      within one fp16 ulp of the exact-sum oracle's and >= 99.9% identical;
+    * the oracle's softmax/PV stage on the kernel's own fp16 scores is within
+      max-abs 2e-3 / mean-abs 2e-4 of the kernel's output."""
+    q, k, v, cu, bits, out, hq, hk = (cfg2[x] for x in ("q", "k", "v", "cu", "bits", "out", "hq", "hk"))
+    s0 = int(cu[z])
+    rows, kend = BM, m * BM + BM
+    qs, ks, vs = q[s0 + m * BM:s0 + kend], k[s0:s0 + kend], v[s0:s0 + kend]
+    cuq, cuk = np.array([0, rows], dtype=np.int32), np.array([0, kend], dtype=np.int32)
+    sub_bits = np.array([int(bits[h * 32 + m]) for h in range(hk)], dtype=np.uint64)
+    q8, sq, cuqs = O.quant_per_block_int8(qs, cuq, 128)
+    k8, sk, cuks = O.quant_per_block_int8(ks, cuk, 64)
+    o_sub, qk_i32, qk16 = tmx.debug_launch(
+        to_dev(qs, device), to_dev(ks, device), to_dev(vs, device), to_dev(cuq, device), to_dev(cuk, device),
+        rows, kend, bitmask_tensor(sub_bits, device), q8=to_dev(q8, device), k8=to_dev(k8, device),
+        sQ_blocks=to_dev(sq.astype(np.float16), device), sK_blocks=to_dev(sk.astype(np.float16), device),
+        cu_q_scale=to_dev(cuqs.astype(np.int32), device), cu_k_scale=to_dev(cuks.astype(np.int32), device),
+        block_m=BM, block_n_mask=64, causal=True, routing_mode="mixed", q_in_kernel=True)
+    torch.cuda.synchronize()
+    o_sub = o_sub.cpu().numpy()
+    np.testing.assert_array_equal(o_sub.view(np.uint16), out[s0 + m * BM:s0 + kend].view(np.uint16))
+    gi, gf = qk_i32.cpu().numpy(), qk16.cpu().numpy()
+    ref_out, scores = O.attn_fwd(qs, ks, vs, cuq, cuk, sub_bits, block_m=BM, block_n_mask=64, causal=True,
+                                 q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
+                                 cu_q_scale=cuqs, cu_k_scale=cuks, want_scores=True)
+    valid = np.arange(kend)[None, :] <= np.arange(rows)[:, None] + (kend - rows)
+    n_f16 = n_i8 = same16 = 0
+    for h in range(hq):
+        acc, s16, route = scores[(0, h)]
+        sel8 = valid & route
+        np.testing.assert_array_equal(gi[:, h][sel8], acc[sel8].astype(np.int32))
+        np.testing.assert_array_equal(gf[:, h][sel8].view(np.uint16), s16[sel8].view(np.uint16))
+        self16 = valid & ~route
+        a, b = gf[:, h][self16].astype(np.float32), s16[self16].astype(np.float32)
+        ulp = np.abs(np.spacing(b.astype(np.float16)).astype(np.float32))
+        assert (np.abs(a - b) <= np.maximum(ulp, 2.0 ** -10)).all()
+        same16 += int((a == b).sum())
+        n_f16 += int(self16.sum())
+        n_i8 += int(sel8.sum())
+    assert n_f16 > 0 and n_i8 > 0
+    print(f"cfg2 block ({z},{m}): {n_i8} INT8-route int32 accumulators and fp16 scores bit-exact; "
+          f"{same16 / n_f16:.5f} of {n_f16} FP16-route scores identical to the exact sum's", flush=True)
+    assert same16 / n_f16 >= 0.999
+    ref_given = O.attn_fwd(qs, ks, vs, cuq, cuk, sub_bits, block_m=BM, block_n_mask=64, causal=True,
+                           q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
+                           cu_q_scale=cuqs, cu_k_scale=cuks, qk16_override=lambda zz, hh: gf[:, hh])
+    d = np.abs(o_sub.astype(np.float64) - ref_given.astype(np.float64))
+    _report(f"cfg2 block ({z},{m}) kernel vs oracle softmax/PV on the kernel's scores", d)
+    assert_close_out(o_sub, ref_given)
+
+
+@pytest.fixture(scope="module")
+def cfg3_inputs():
     L, hq, hk = 32768, 28, 4
     q, k, v, cu = _inputs([L], hq, hk, 128, seed=3, head_scale=True)
+    return q, k, v, cu, hq, hk
+
+
+@pytest.mark.parametrize("pattern", ["row_rand", "bigbird"])
+def test_cfg3_full_size_blocks(device, cfg3_inputs, pattern):
+    """B1 x 32768, Hq28/Hk4 (Qwen2-7B), D128, per-head scales, row_rand / bigbird 0.5, mask groups of 8."""
+    q, k, v, cu, hq, hk = cfg3_inputs
+    L = int(cu[-1])
     bnm = 512
-    bits = _row_map(L, bnm, "row_rand", {}, hk)
+    bits = _row_map(L, bnm, pattern, {}, hk)
     out = _launch(q, k, v, cu, bits, bnm, device)
     assert np.isfinite(out).all()
     for m in (0, 100, 255):  # 255: the last query block, 32768 keys
         ref = _oracle_block(q, k, v, cu, bits, hk, 0, m, bnm)
         got = out[m * BM:m * BM + ref.shape[0]]
+        _report(f"cfg3 {pattern} block {m}", np.abs(got.astype(np.float64) - ref.astype(np.float64)))
         assert_close_out(got, ref)
 
 
@@ -132,7 +178,9 @@ def test_cfg4_packed_varlen(device):
         for m in sorted({0, mb - 1}):
             ref = _oracle_block(q, k, v, cu, bits, hk, z, m, bnm)
             s = int(cu[z]) + m * BM
-            assert_close_out(out[s:s + ref.shape[0]], ref)
+            got = out[s:s + ref.shape[0]]
+            _report(f"cfg4 seq {z} (L={L}) block {m}", np.abs(got.astype(np.float64) - ref.astype(np.float64)))
+            assert_close_out(got, ref)
         # the same sequence launched alone: identical rows
         s0, s1 = int(cu[z]), int(cu[z + 1])
         alone = _launch(q[s0:s1], k[s0:s1], v[s0:s1], np.array([0, L], dtype=np.int32), bits[:hk * mb], bnm,

@@ -20,9 +20,10 @@ pytestmark = pytest.mark.gpu
 
 
 def _oracle_varlen_attention(q, k, v, block_m, block_n, *, block_n_mask=None, causal, scale, precision_map_all,
-                             candidates=None, flat_lengths=None, bias=None):
+                             candidates=None, flat_lengths=None, bias=None, fp16_accum="exact"):
     """tilemix_varlen_attention computed by the CPU oracle (mixed routing,
-    BLKQ 128 / BLKK 64, fp16 V for PV: the defaults of the dense entry)."""
+    BLKQ 128 / BLKK 64, fp16 V for PV: the defaults of the dense entry);
+    ``fp16_accum`` selects the oracle's FP16-route score accumulation model."""
     B, Hq, T, D = q.shape
     Hk = k.shape[1]
     qn = q.permute(0, 2, 1, 3).reshape(B * T, Hq, D).float().cpu().numpy().astype(np.float16)
@@ -34,7 +35,7 @@ def _oracle_varlen_attention(q, k, v, block_m, block_n, *, block_n_mask=None, ca
     bits = np.array([int(x) for x in precision_map_all.reshape(-1).tolist()], dtype=np.uint64)
     out = O.attn_fwd(qn, kn, vn, cu, cu, bits, block_m=block_m, block_n_mask=block_n_mask or block_n,
                      causal=causal, sm_scale=scale, q8=q8, k8=k8, sq16=sq.astype(np.float16),
-                     sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk)
+                     sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk, fp16_accum=fp16_accum)
     o = torch.from_numpy(out.astype(np.float32)).to(q.device, torch.float16)
     return o.view(B, T, Hq, D).permute(0, 2, 1, 3)
 

@@ -267,3 +267,20 @@ def test_q_in_kernel_rule():
     assert tmx._q_in_kernel_supported(64, 128, int8, False)
     assert not tmx._q_in_kernel_supported(64, 128, mixed, False)
     assert not tmx._q_in_kernel_supported(128, 64, mixed, True)
+
+
+def test_int8_views_are_copied_to_16_byte_strides():
+    """q8/k8/v8 are streamed as 16-byte vectors: a view whose token or head
+    stride is not a multiple of 16 bytes (here 8 mod 16) is replaced by a dense
+    copy, an aligned one is passed through (the C layer rejects other strides)."""
+    base = torch.zeros(10, 3, 136, dtype=torch.int8)
+    view = base[..., :128]
+    assert view.stride(1) % 16 == 8
+    fixed = tmx._inner_contiguous(view, 16)
+    assert fixed.stride(0) % 16 == 0 and fixed.stride(1) % 16 == 0 and fixed.is_contiguous()
+    aligned = torch.zeros(10, 3, 144, dtype=torch.int8)[..., :128]
+    assert tmx._inner_contiguous(aligned, 16) is aligned
+    src = (Path(tmx.__file__)).read_text()
+    # every int8 operand goes through the 16-byte rule before the launch
+    assert "_inner_contiguous(v8, 16)" in src and "_inner_contiguous(k8, 16)" in src
+    assert "_inner_contiguous(q8, 16)" in src

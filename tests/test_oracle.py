@@ -1,8 +1,10 @@
 """Pin the CPU oracle (oracle/tilemix_oracle.py) before trusting it as the checker.
 
-The reference ships no golden vectors for the attention path (its own tests
-cover the routing maps only, see test_precision_maps.py), so every oracle
-function is checked here against something that does not restate its formula:
+The reference ships no tests and no golden vectors (the routing-map fixtures
+of test_precision_maps.py were written by this repository's
+tests/golden/make_precision_map_goldens.py from the reference's own module), so
+every oracle function is checked here against something that does not restate
+its formula:
 
 * quantisation: closed-form invariants, exact half-way rounding cases, and an
   element-by-element scalar restatement on small blocks;

@@ -318,7 +318,7 @@ def launch_prequantized(
         p.k8, p.sk, p.cu_k_scale = k8c.data_ptr(), sk.data_ptr(), cks.data_ptr()
         p.stride_k8_token, p.stride_k8_head = k8c.stride(0), k8c.stride(1)
         if not int8_use_fp16_v:
-            v8c = _inner_contiguous(v8, 8)
+            v8c = _inner_contiguous(v8, 16)
             sv = sV_blocks.to(torch.float16).contiguous()
             cvs = cu_v_scale.to(dtype=torch.int32).contiguous()
             keep += [v8c, sv, cvs]

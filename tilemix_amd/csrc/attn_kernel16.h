@@ -175,13 +175,18 @@ attn16_kernel(const AttnKArgs a) {
   const unsigned char* v8seq = INT8V
       ? reinterpret_cast<const unsigned char*>(a.v8 + (int64_t)k_start * a.sv8_t + (int64_t)hk * a.sv8_h) : nullptr;
   // 0 = K (fp16 or int8) and int8 V codes, 1 = V fp16.
+  // A lane whose 16-byte row chunk lies at or past head_dim gets an offset
+  // beyond every buffer's size: the copy writes zeros there and never reads a
+  // byte outside [0, head_dim) of a row.
   auto lane_off = [&](int L, int rowb, int64_t tok_bytes, int kind) -> int {
     const int rpi = 1024 / rowb, cpr = rowb / 16;
     const int r = L * rpi + lane / cpr;
     int sw;
     if (kind == 1) sw = rowb == 256 ? swz_v<256>(r) : swz_v<128>(r);
     else sw = rowb == 256 ? swz_k<256>(r) : rowb == 128 ? swz_k<128>(r) : swz_k<64>(r);
-    return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
+    const int chunk = (lane % cpr) ^ sw;  // the row chunk this lane copies
+    if (chunk * 16 >= (rowb == ROW16 ? 2 * a.d : a.d)) return kOffOutside;
+    return (int)(r * tok_bytes) + chunk * 16;
   };
   // Copies are issued from inline assembly (async_load16_asm): the loop
   // orders them against its LDS reads itself (s_waitcnt + barrier per tile).

@@ -141,19 +141,26 @@ attn32_kernel(const AttnKArgs a) {
       ? reinterpret_cast<const unsigned char*>(a.k8 + (int64_t)k_start * a.sk8_t + (int64_t)hk * a.sk8_h) : nullptr;
   const unsigned char* v8seq = INT8V
       ? reinterpret_cast<const unsigned char*>(a.v8 + (int64_t)k_start * a.sv8_t + (int64_t)hk * a.sv8_h) : nullptr;
-  auto lane_off0 = [&](int rowb, int64_t tok_bytes, bool vswz) -> int {
+  // A lane whose 16-byte row chunk lies at or past head_dim (columns the
+  // padded tile width adds) gets an offset beyond every buffer's size, so the
+  // copy writes zeros there: no byte outside [0, head_dim) of a row is ever
+  // read, and the padded columns are finite (0 * x = 0 in the MFMAs).  The
+  // swizzle of copy i's rows is that of copy 0's, so the chunk is per lane.
+  auto lane_off0 = [&](int rowb, int64_t tok_bytes, bool vswz, int valid_bytes) -> int {
     const int rpi = 1024 / rowb, cpr = rowb / 16;
     const int r = wave * rpi + lane / cpr;
     int sw;
     if (rowb == 256) sw = vswz ? swz_v32<256>(r) : swz_k<256>(r);
     else if (rowb == 128) sw = vswz ? swz_v32<128>(r) : swz_k<128>(r);
     else sw = swz_k<64>(r);
-    return (int)(r * tok_bytes) + ((lane % cpr) ^ sw) * 16;
+    const int chunk = (lane % cpr) ^ sw;  // the row chunk this lane copies
+    if (chunk * 16 >= valid_bytes) return kOffOutside;
+    return (int)(r * tok_bytes) + chunk * 16;
   };
-  const int dma_k16 = lane_off0(ROW16, kt_bytes, false);
-  const int dma_k8 = MODE != TILEMIX_ROUTING_FP16 ? lane_off0(ROW8, k8t_bytes, false) : 0;
-  const int dma_v16 = lane_off0(ROW16, vt_bytes, true);
-  const int dma_v8 = INT8V ? lane_off0(ROW8, v8t_bytes, false) : 0;
+  const int dma_k16 = lane_off0(ROW16, kt_bytes, false, 2 * a.d);
+  const int dma_k8 = MODE != TILEMIX_ROUTING_FP16 ? lane_off0(ROW8, k8t_bytes, false, a.d) : 0;
+  const int dma_v16 = lane_off0(ROW16, vt_bytes, true, 2 * a.d);
+  const int dma_v8 = INT8V ? lane_off0(ROW8, v8t_bytes, false, a.d) : 0;
   const int step_k16 = NW * (1024 / ROW16) * (int)kt_bytes;
   const int step_k8 = NW * (1024 / ROW8) * (int)k8t_bytes;
   const int step_v16 = NW * (1024 / ROW16) * (int)vt_bytes;
