@@ -95,9 +95,11 @@ int tilemix_quant_per_block_int8(const tilemix_quant_params* p, void* stream);
  * Replaces attn_fwd (attention/triton/tilemix.py:503-951) launched by
  * launch_prequantized (:1132-1337).  One launch computes, for every sequence z,
  * query head h and query block m (block_m rows), the causal/varlen
- * online-softmax attention over key tiles of block_n = 64 keys, routing each
- * tile group (block_n_mask keys) to FP16 or INT8 QK^T by bit j of
- * precision_bitmask[hk * ceil(Lq_z / block_m) + m] (hk = h / (heads_q/heads_k)).
+ * online-softmax attention over key tiles of block_n keys (one softmax step
+ * per tile), routing each tile group (block_n_mask keys) to FP16 or INT8 QK^T
+ * by bit j of precision_bitmask[hk * ceil(Lq_z / block_m) + m]
+ * (hk = h / (heads_q/heads_k)).  The K (and V) scale of key n is
+ * sk[cu_k_scale[z] + n / blkk], clamped to the sequence's last scale row.
  *
  * q_quant_in_kernel = 1 (blkq == 128, routing not FP16, and block_m == 128 or
  * block_m == 64 unless mixed routing runs on int8 V codes): each 128-row
@@ -107,9 +109,12 @@ int tilemix_quant_per_block_int8(const tilemix_quant_params* p, void* stream);
  * reading q8/sq/cu_q_scale, which may then be NULL.  This removes the Q
  * pre-pass of tilemix_attention_with_quant; the reference has no such field.
  *
- * Supported by this build: block_m in {64, 128}; block_n == 64;
- * block_n_mask a multiple of 64 with ceil(max_seqlen_k/block_n_mask) <= 64;
- * head_dim a multiple of 16, <= 128; blkk a multiple of 64; fp16 data.
+ * Supported by this build: block_m in {64, 128}; block_n in {64, 128, 256};
+ * block_n_mask a multiple of block_n with ceil(max_seqlen_k/block_n_mask) <= 64;
+ * head_dim a multiple of 16, <= 128 (the Python layer zero-pads other widths);
+ * blkk a positive multiple of 4; fp16 data.  block_n = 64 with blkk a multiple
+ * of 64 runs the fastest kernels; other shapes run variants that stream each
+ * block_n tile twice (max pass, then update pass) and look scales up per key.
  */
 typedef struct tilemix_attn_params {
     const void* q;                /* fp16 [tokens_q, heads_q, head_dim]            */

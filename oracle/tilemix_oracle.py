@@ -28,9 +28,10 @@ Numerics contract (what the HIP kernel must reproduce):
 4. INT8 tile: acc = sum_d q8 k8 (exact int32);  ss = fp16(fp32(fp16(sq sk)) qk_scale);
    qk = fp16(fp32(acc) fp32(ss))                                 (:380-404)
 5. invalid (key >= Lk, or causal key > row + Lk - Lq) -> -inf     (:256-262)
-6. online softmax per 64-key tile in ascending key order: m' = max(m, max qk),
-   p = fp16(exp2(qk - m')), l = l alpha + sum fp32(p), acc = acc alpha + p.V
-   (fp32), alpha = exp2(m - m'); l starts at 1.0                 (:179-207,727-729)
+6. online softmax per block_n-key tile (64, 128 or 256) in ascending key order:
+   m' = max(m, max qk over the tile), p = fp16(exp2(qk - m')), l = l alpha +
+   sum fp32(p), acc = acc alpha + p.V (fp32), alpha = exp2(m - m'); l starts at
+   1.0                                                       (:179-207,727-729)
 7. out = fp16(acc / l)                                           (:935-951)
 
 Tiles beyond a query block's causal tile count are fully masked for every row
@@ -207,7 +208,7 @@ def attn_fwd(q, k, v, cu_q, cu_k, bitmask, *, block_m: int, block_n_mask: int, c
              q8=None, k8=None, sq16=None, sk16=None, cu_q_scale=None, cu_k_scale=None,
              blkq: int = 128, blkk: int = 64, int8_use_fp16_v: bool = True,
              v8=None, sv16=None, cu_v_scale=None, bias=None, want_scores: bool = False,
-             qk16_override=None, fp16_accum: str = "exact"):
+             qk16_override=None, fp16_accum: str = "exact", block_n: int = 64):
     """fp32 emulation of attn_fwd over packed varlen [tokens, heads, dim] fp16 input.
 
     Returns out (float16, shape of q); with want_scores also a dict mapping
@@ -216,7 +217,13 @@ def attn_fwd(q, k, v, cu_q, cu_k, bitmask, *, block_m: int, block_n_mask: int, c
     [Lq, Lk] or None) replaces the score stage, so the softmax/PV stage can be
     checked on given scores.  ``fp16_accum`` is the accumulation of the FP16
     route's dot(q16, k) before its fp16 rounding (see ``fp16_tile_scores``).
+    ``block_n`` is the key width of one online-softmax step (the reference's
+    BLOCK_N, :603-615); route bits and K/V scales are per key, so it changes
+    only where the running maximum is updated (block_n_mask % block_n == 0,
+    :578-583).
     """
+    if block_n % BN or block_n_mask % block_n:
+        raise ValueError(f"block_n ({block_n}) must be a multiple of 64 dividing block_n_mask ({block_n_mask})")
     q = np.asarray(q)
     k = np.asarray(k)
     v = np.asarray(v)
@@ -236,7 +243,7 @@ def attn_fwd(q, k, v, cu_q, cu_k, bitmask, *, block_m: int, block_n_mask: int, c
         ks, Lk = int(cu_k[z]), int(cu_k[z + 1] - cu_k[z])
         if Lq == 0:
             continue
-        nt = _ceil_div(Lk, BN)
+        nt = _ceil_div(Lk, block_n)
         rows = np.arange(Lq)
         keys = np.arange(Lk)
         valid = np.broadcast_to(keys[None, :] < Lk, (Lq, Lk)).copy()
@@ -279,7 +286,7 @@ def attn_fwd(q, k, v, cu_q, cu_k, bitmask, *, block_m: int, block_n_mask: int, c
                 s = np.where(valid, (s.astype(f16).astype(f32) + bl.astype(f32)).astype(f16).astype(f32), s)
             if want_scores:
                 scores[(z, h)] = (acc_i32, qk16, route)
-            # ---- online softmax, one 64-key tile at a time ------------------
+            # ---- online softmax, one block_n-key tile at a time -------------
             m_i = np.full(Lq, -np.inf, dtype=f32)
             l_i = np.ones(Lq, dtype=f32)
             acc = np.zeros((Lq, dim), dtype=f32)
@@ -288,7 +295,7 @@ def attn_fwd(q, k, v, cu_q, cu_k, bitmask, *, block_m: int, block_n_mask: int, c
                 sv = _scale_rows(np.asarray(sv16), int(cu_v_scale[z]), int(cu_v_scale[z + 1]),
                                  keys // blkk, hk)
             for n in range(nt):
-                k0, k1 = n * BN, min((n + 1) * BN, Lk)
+                k0, k1 = n * block_n, min((n + 1) * block_n, Lk)
                 st = s[:, k0:k1]
                 mx = st.max(axis=1)
                 has = mx != -np.inf

@@ -201,13 +201,14 @@ def check_int8_attention(Om):
     assert err.max() < 4e-3 and err.mean() < 4e-4, (err.max(), err.mean())
 
 
-def check_single_tile(Om):
+def _single_tile(Om, L, block_n):
     # One tile: m = row max, alpha = 0 on the first tile, l = sum fp16(p).
-    q, k, v, cu_q, cu_k = _inputs([48], 1, 1, 32, seed=5, scale=2.0)
-    out = Om.attn_fwd(q, k, v, cu_q, cu_k, _all_bits(1, 1, 0), block_m=64, block_n_mask=64, causal=True)
+    q, k, v, cu_q, cu_k = _inputs([L], 1, 1, 32, seed=5, scale=2.0)
+    out = Om.attn_fwd(q, k, v, cu_q, cu_k, _all_bits(1, -(-L // 64), 0), block_m=64, block_n_mask=256,
+                      causal=True, block_n=block_n)
     qk_scale = f32(f32(32 ** -0.5) * f32(O.LOG2E))
     q16 = (q[:, 0].astype(f32) * qk_scale).astype(f16)
-    for r in range(48):
+    for r in range(0, L, max(1, L // 48)):
         s = [f16(np.dot(q16[r].astype(np.float64), k[j, 0].astype(np.float64))) for j in range(r + 1)]
         m = max(float(x) for x in s)
         p = [f16(np.exp2(f32(f32(x) - f32(m)))) for x in s]
@@ -215,6 +216,84 @@ def check_single_tile(Om):
         num = sum(float(p[j]) * v[j, 0].astype(np.float64) for j in range(r + 1))
         ref = num / den
         assert np.abs(out[r, 0].astype(np.float64) - ref).max() <= 2.0 ** -10 * max(1.0, np.abs(ref).max())
+
+
+def check_single_tile(Om):
+    _single_tile(Om, 48, 64)
+
+
+def check_single_tile_block_n256(Om):
+    # 200 keys are one softmax step at block_n = 256.
+    _single_tile(Om, 200, 256)
+
+
+def check_block_n_known_answer(Om):
+    """One row of 65 keys with given fp16 scores 0 (keys 0-63) and 0.5 (key 64),
+    V = 1 on keys 0-63 and -45 on key 64.  block_n >= 128 is one softmax step:
+    m = 0.5 before any p, p = fp16(2^-0.5) on keys 0-63, so
+    out = (64 p - 45) / (64 p + 1).  block_n = 64 takes p = 1 under m = 0 and
+    then rescales by alpha = fp32(2^-0.5): out = (64 alpha - 45) / (64 alpha + 1).
+    The two differ by ~1e-4 (~27 fp16 ulps of the output)."""
+    L = 65
+    q = np.zeros((L, 1, 16), f16)
+    k = np.zeros((L, 1, 16), f16)
+    v = np.zeros((L, 1, 16), f16)
+    v[:64, 0, 0] = 1
+    v[64, 0, 0] = -45
+    s = np.zeros((L, L), f16)
+    s[:, 64] = 0.5
+    cu = np.array([0, L])
+    got = {}
+    for bn in (64, 128, 256):
+        out = Om.attn_fwd(q, k, v, cu, cu, _all_bits(1, 2, 0), block_m=64, block_n_mask=256, causal=False,
+                          qk16_override=lambda z, h: s, block_n=bn)
+        assert (out[:, 0, 0] == out[0, 0, 0]).all()
+        got[bn] = out[0, 0, 0]
+    p = f32(f16(np.exp2(f32(-0.5))))
+    alpha = f32(np.exp2(f32(-0.5)))
+    want_one_step = f16(f32(f32(64) * p - f32(45)) / f32(f32(64) * p + f32(1)))
+    want_two_steps = f16(f32(f32(64) * alpha - f32(45)) / f32(f32(64) * alpha + f32(1)))
+    assert want_one_step != want_two_steps
+    assert got[128] == want_one_step and got[256] == want_one_step, (got, want_one_step)
+    assert got[64] == want_two_steps, (got, want_two_steps)
+
+
+def check_block_n_fp16_attention(Om):
+    # block_n 128 / 256 against fp64 softmax attention (varlen, causal, GQA).
+    q, k, v, cu_q, cu_k = _inputs([300, 129, 1], 4, 2, 64, seed=12)
+    for bn in (128, 256):
+        out = Om.attn_fwd(q, k, v, cu_q, cu_k, _all_bits(2, 5, 0), block_m=64, block_n_mask=256, causal=True,
+                          block_n=bn)
+        ref = _fp64_attention(q, k, v, cu_q, cu_k, True)
+        err = np.abs(out.astype(np.float64) - ref)
+        assert err.max() < 4e-3 and err.mean() < 4e-4, (bn, err.max(), err.mean())
+
+
+def check_int8_vector_scales(Om):
+    """INT8 route with K scale blocks of 16, 32 and 48 keys (the per-key lookup
+    sk[key // BLKK], reference :390) and block_n 128: fp64 attention over the
+    dequantised scores."""
+    q, k, v, cu_q, cu_k = _inputs([150, 70], 4, 2, 64, seed=13)
+    q8, sq, cuq = Om.quant_per_block_int8(q, cu_q, 128)
+    sq16 = sq.astype(f16)
+    for blkk, bn in ((16, 64), (32, 128), (48, 64)):
+        k8, sk, cuk = Om.quant_per_block_int8(k, cu_k, blkk)
+        sk16 = sk.astype(f16)
+        out = Om.attn_fwd(q, k, v, cu_q, cu_k, _all_bits(2, 3, ~np.uint64(0)), block_m=64, block_n_mask=128,
+                          causal=True, routing_mode=O.ROUTING_INT8, q8=q8, k8=k8, sq16=sq16, sk16=sk16,
+                          cu_q_scale=cuq, cu_k_scale=cuk, blkk=blkk, block_n=bn)
+
+        def scores(z, h):
+            qa = q8[cu_q[z]:cu_q[z + 1], h].astype(np.float64)
+            ka = k8[cu_k[z]:cu_k[z + 1], h // 2].astype(np.float64)
+            lq, lk = qa.shape[0], ka.shape[0]
+            rq = sq16[cuq[z] + np.arange(lq) // 128, h].astype(np.float64)
+            rk = sk16[cuk[z] + np.arange(lk) // blkk, h // 2].astype(np.float64)
+            return (qa @ ka.T) * rq[:, None] * rk[None, :] * 64 ** -0.5
+
+        ref = _fp64_attention(q, k, v, cu_q, cu_k, True, scores=scores)
+        err = np.abs(out.astype(np.float64) - ref)
+        assert err.max() < 4e-3 and err.mean() < 4e-4, (blkk, err.max(), err.mean())
 
 
 def check_route_table(Om):
@@ -231,7 +310,8 @@ def check_route_table(Om):
 
 CHECKS = [check_quant_invariants, check_quant_halfway, check_quant_bruteforce, check_quant_zero_and_tail,
           check_int32_accumulators, check_fp16_attention, check_int8_attention, check_single_tile,
-          check_route_table]
+          check_single_tile_block_n256, check_block_n_known_answer, check_block_n_fp16_attention,
+          check_int8_vector_scales, check_route_table]
 
 
 @pytest.mark.parametrize("check", CHECKS, ids=[c.__name__ for c in CHECKS])
@@ -249,14 +329,20 @@ MUTATIONS = {
     "dequant_no_qk_scale": ("ss = (sqk.astype(f32) * qk_scale).astype(f16)",
                             "ss = (sqk.astype(f32) * f32(O_LOG2E_ONLY)).astype(f16)"),
     "inverted_alpha": ("np.exp2(m_i - m_next)", "np.exp2(m_next - m_i)"),
+    # softmax steps of 64 keys whatever block_n is (every key still visited)
+    "softmax_step_64": [("nt = _ceil_div(Lk, block_n)", "nt = _ceil_div(Lk, BN)"),
+                        ("k0, k1 = n * block_n, min((n + 1) * block_n, Lk)", "k0, k1 = n * BN, min((n + 1) * BN, Lk)")],
+    "k_scale_block_64": ("int(cu_k_scale[z + 1]),\n                                 keys // blkk",
+                         "int(cu_k_scale[z + 1]),\n                                 keys // 64"),
 }
 
 
 def _mutant(name):
     src = open(O.__file__).read()
-    old, new = MUTATIONS[name]
-    assert src.count(old) == 1, f"mutation anchor for {name} not unique"
-    src = src.replace(old, new)
+    pairs = MUTATIONS[name]
+    for old, new in ([pairs] if isinstance(pairs, tuple) else pairs):
+        assert src.count(old) == 1, f"mutation anchor for {name} not unique"
+        src = src.replace(old, new)
     mod = types.ModuleType(f"oracle_mutant_{name}")
     mod.__dict__["O_LOG2E_ONLY"] = O.LOG2E
     exec(compile(src, f"<mutant {name}>", "exec"), mod.__dict__)

@@ -14,6 +14,12 @@ same public names, arguments, return values and validation errors --
 C ABI (include/tilemix_hip.h); there is no Triton and no CPU fallback.
 
 Differences that do not change results:
+* a head_dim that is not a multiple of 16 is zero-padded to the next multiple
+  of 16 on the host (Q, K, V and their int8 codes) and the output is copied
+  back at the original width: zero columns add 0 to every dot product and do
+  not change a block's max|x|, where the reference masks the columns past
+  head_dim inside the kernel (:252, :364, :639); sm_scale defaults to
+  head_dim ** -0.5 of the original width;
 * the scale tensors used inside ``tilemix_attention_with_quant`` are sized
   from the token count (no device->host read of the scale-row count);
 * Triton's autotune table is replaced by a fixed gfx950 tiling, so
@@ -40,9 +46,12 @@ ROUTING_MODE_FP16 = _native.ROUTING_FP16
 ROUTING_MODE_INT8 = _native.ROUTING_INT8
 RoutingMode = Literal["auto", "mixed", "fp16", "int8"]
 
-# Tile sizes the gfx950 kernel is instantiated for.
+# Tile sizes the gfx950 kernel is instantiated for (block_n > 64 runs as
+# 64-key tiles with the reference's per-block_n softmax step).
 SUPPORTED_BLOCK_M = (64, 128)
-SUPPORTED_BLOCK_N = (64,)
+SUPPORTED_BLOCK_N = (64, 128, 256)
+# The kernel's head-dim granularity; other widths are zero-padded to it.
+HEAD_DIM_MULTIPLE = 16
 
 
 def _scale_dtype(dtype: torch.dtype) -> torch.dtype:
@@ -174,6 +183,19 @@ def _dummy_v_quantization_metadata(v, cu_seqlens_k):
     return v8, sv, cuv
 
 
+def _padded_head_dim(head_dim: int) -> int:
+    return -(-head_dim // HEAD_DIM_MULTIPLE) * HEAD_DIM_MULTIPLE
+
+
+def _pad_head_dim(t: Optional[torch.Tensor], width: int) -> Optional[torch.Tensor]:
+    """[tokens, heads, d] -> a dense [tokens, heads, width] copy, zeros past d."""
+    if t is None or t.shape[-1] == width:
+        return t
+    out = torch.zeros((*t.shape[:-1], width), dtype=t.dtype, device=t.device)
+    out[..., :t.shape[-1]] = t
+    return out
+
+
 def _inner_contiguous(t: torch.Tensor, align: int) -> torch.Tensor:
     """The kernel reads 16-byte vectors along the head dim: unit dim stride and
     vector-aligned token/head strides; otherwise take a dense copy."""
@@ -269,21 +291,23 @@ def launch_prequantized(
     padded_head_dim = ((padded_head_dim + 31) // 32) * 32
     if padded_head_dim > 128:
         raise ValueError("head dimension must be <= 128")
-    if head_dim % 16:
-        raise ValueError(f"the HIP TileMix kernel needs head_dim % 16 == 0, got {head_dim}")
-    if mode_code != ROUTING_MODE_FP16 and BLKK % 64:
-        raise ValueError(f"the HIP TileMix kernel needs BLKK % 64 == 0, got {BLKK}")
+    if mode_code != ROUTING_MODE_FP16 and (BLKK <= 0 or BLKK % 4):
+        raise ValueError(f"the HIP TileMix kernel needs BLKK to be a positive multiple of 4, got {BLKK}")
     _forced_config_check(block_m, block_n)
 
     if sm_scale is None:
-        sm_scale = q.shape[-1] ** -0.5
+        sm_scale = head_dim ** -0.5
     out_user = o
     if o is None:
         o = torch.empty_like(q)
+    run_dim = _padded_head_dim(head_dim)
+    if run_dim != head_dim:
+        q, k, v = (_pad_head_dim(t, run_dim) for t in (q, k, v))
+        q8, k8, v8 = (_pad_head_dim(t, run_dim) for t in (q8, k8, v8))
     q = _inner_contiguous(q, 8)
     k = _inner_contiguous(k, 8)
     v = _inner_contiguous(v, 8)
-    o_dev = o if (o.stride(2) == 1 and o.stride(0) % 4 == 0 and o.stride(1) % 4 == 0
+    o_dev = o if (run_dim == head_dim and o.stride(2) == 1 and o.stride(0) % 4 == 0 and o.stride(1) % 4 == 0
                   and o.data_ptr() % 8 == 0) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
     device = q.device
     cu_seqlens_q = cu_seqlens_q.to(device=device, dtype=torch.int32).contiguous()
@@ -330,7 +354,7 @@ def launch_prequantized(
         p.bias = b.data_ptr()
         p.stride_bias_head, p.stride_bias_m, p.stride_bias_n = b.stride(1), b.stride(2), b.stride(3)
     p.sm_scale = float(sm_scale)
-    p.heads_q, p.heads_k, p.head_dim, p.batch = heads_q, heads_k, head_dim, batch
+    p.heads_q, p.heads_k, p.head_dim, p.batch = heads_q, heads_k, run_dim, batch
     p.max_seqlen_q, p.max_seqlen_k = int(max_seqlens_q), int(max_seqlens_k)
     p.block_m, p.block_n, p.block_n_mask = int(block_m), int(block_n), int(block_n_mask)
     p.blkq, p.blkk = int(BLKQ), int(BLKK)
@@ -340,7 +364,7 @@ def launch_prequantized(
     if batch > 0:
         _native.attn_fwd(p, device)
     if o_dev is not o:
-        o.copy_(o_dev)
+        o.copy_(o_dev[..., :head_dim])
     del keep
     if out_user is not None:
         return out_user, normalized_mode
@@ -365,9 +389,23 @@ def tilemix_attention_with_quant(
 
     Quantisation here uses the no-sync path: fp16 scales are written by the
     quantisation kernel and its scale-row prefix is computed on the device.
+    A head_dim that is not a multiple of 16 is zero-padded before quantising
+    (codes and scales of the real columns are unchanged).
     """
     if block_n_mask is None:
         block_n_mask = block_n
+    head_dim = q.shape[-1]
+    run_dim = _padded_head_dim(head_dim)
+    if run_dim != head_dim and q.ndim == 3 and k.ndim == 3 and v.ndim == 3 and run_dim <= 128:
+        if sm_scale is None:
+            sm_scale = head_dim ** -0.5
+        out, mode = tilemix_attention_with_quant(
+            _pad_head_dim(q, run_dim), _pad_head_dim(k, run_dim), _pad_head_dim(v, run_dim),
+            cu_seqlens_q, cu_seqlens_k, max_seqlens_q, max_seqlens_k, precision_bitmask,
+            block_m=block_m, block_n=block_n, block_n_mask=block_n_mask, BLKQ=BLKQ, BLKK=BLKK,
+            causal=causal, sm_scale=sm_scale, bias=bias, routing_mode=routing_mode, run_length=run_length,
+            scalar_scales=scalar_scales, int8_cache_ca=int8_cache_ca, int8_use_fp16_v=int8_use_fp16_v)
+        return out[..., :head_dim].contiguous(), mode
     normalized_mode = routing_mode.strip().lower()
     if normalized_mode == "auto":
         normalized_mode = classify_bitmask_routing(
@@ -422,7 +460,8 @@ def _q_in_kernel_enabled() -> bool:
 
 def debug_launch(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlens_q, max_seqlens_k, precision_bitmask,
                  *, q8, k8, sQ_blocks, sK_blocks, cu_q_scale, cu_k_scale, block_m, block_n_mask,
-                 BLKQ=128, BLKK=64, causal=True, sm_scale=None, routing_mode="mixed", q_in_kernel=False):
+                 BLKQ=128, BLKK=64, causal=True, sm_scale=None, routing_mode="mixed", q_in_kernel=False,
+                 block_n=64):
     """Run the kernel's DUMP instantiation (C entry ``tilemix_attn_fwd_debug``).
 
     Returns ``(out, qk_i32 [tokens_q, Hq, max_k] int32, qk16 [tokens_q, Hq, max_k] fp16)``;
@@ -462,7 +501,7 @@ def debug_launch(q, k, v, cu_seqlens_q, cu_seqlens_k, max_seqlens_q, max_seqlens
     p.heads_q, p.heads_k, p.head_dim = q.shape[1], k.shape[1], q.shape[2]
     p.batch = cu_q.numel() - 1
     p.max_seqlen_q, p.max_seqlen_k = int(max_seqlens_q), int(max_seqlens_k)
-    p.block_m, p.block_n, p.block_n_mask = int(block_m), 64, int(block_n_mask)
+    p.block_m, p.block_n, p.block_n_mask = int(block_m), int(block_n), int(block_n_mask)
     p.blkq, p.blkk = int(BLKQ), int(BLKK)
     p.causal = 1 if causal else 0
     p.routing_mode = mode_code

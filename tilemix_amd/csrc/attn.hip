@@ -35,8 +35,8 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
     set_error("%s: block_m must be 64 or 128 in this build, got %d", fn, p.block_m);
     return TILEMIX_E_INVALID;
   }
-  if (p.block_n != kBN) {
-    set_error("%s: block_n must be 64 in this build, got %d", fn, p.block_n);
+  if (p.block_n != 64 && p.block_n != 128 && p.block_n != 256) {
+    set_error("%s: block_n must be 64, 128 or 256, got %d", fn, p.block_n);
     return TILEMIX_E_INVALID;
   }
   if (p.block_n_mask <= 0 || p.block_n_mask % p.block_n != 0) {
@@ -85,9 +85,10 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
       set_error("%s: int8 routing needs k8/sk/cu_k_scale", fn);
       return TILEMIX_E_INVALID;
     }
-    if (p.blkq <= 0 || p.blkk <= 0 || p.blkk % kBN != 0) {
-      set_error("%s: BLKQ must be positive and BLKK a multiple of 64 in this build (BLKQ=%d, BLKK=%d)", fn,
-                p.blkq, p.blkk);
+    // A K/V scale block is looked up per 4-key group of keys inside the kernel.
+    if (p.blkq <= 0 || p.blkk <= 0 || p.blkk % 4 != 0) {
+      set_error("%s: BLKQ must be positive and BLKK a positive multiple of 4 (BLKQ=%d, BLKK=%d)", fn, p.blkq,
+                p.blkk);
       return TILEMIX_E_INVALID;
     }
     const bool q8_bad = !p.q_quant_in_kernel && (!aligned(p.q8, 16) || (p.stride_q8_token | p.stride_q8_head) % 16);
@@ -185,9 +186,12 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.group = p.heads_q / p.heads_k;
   a.d = p.head_dim;
   a.m_blocks = m_blocks;
-  a.mask_tiles = p.block_n_mask / p.block_n;
+  a.mask_tiles = p.block_n_mask / kBN;
+  a.ng = p.block_n / kBN;
   a.blkq = p.blkq > 0 ? p.blkq : 1;
   a.blkk = p.blkk > 0 ? p.blkk : kBN;
+  // The block_n = 64 kernels take one K/V scale per 64-key tile.
+  const bool gen = a.ng > 1 || (need_int8 && a.blkk % kBN != 0);
   a.causal = p.causal ? 1 : 0;
   a.q_fused = (need_int8 && p.q_quant_in_kernel) ? 1 : 0;
   const bool dump = dump_i32 != nullptr || dump_f16 != nullptr;
@@ -195,7 +199,7 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.per_xcd = (int)work_items_per_xcd((int64_t)p.heads_k * p.batch, (int64_t)m_blocks * a.group);
 
   const int dp = p.head_dim <= 64 ? 64 : 128;
-  dispatch_attn(a, kind, dp, p.routing_mode, int8v, dump, p.bias != nullptr, stream);
+  dispatch_attn(a, kind, dp, p.routing_mode, int8v, dump, p.bias != nullptr, gen, stream);
   const hipError_t err = hipGetLastError();
   if (err != hipSuccess) {
     set_error("%s: launch failed: %s", fn, hipGetErrorString(err));
@@ -211,12 +215,23 @@ namespace tmx {
 void dispatch_attn_main(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
 void dispatch_attn_bias(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
 void dispatch_attn_dump(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_gen_main(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_gen_bias(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
+void dispatch_attn_gen_dump(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream);
 
-void dispatch_attn(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, bool dump, bool bias,
+void dispatch_attn(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, bool dump, bool bias, bool gen,
                    hipStream_t stream) {
-  if (dump) dispatch_attn_dump(a, kind, dp, mode, int8v, stream);
-  else if (bias) dispatch_attn_bias(a, kind, dp, mode, int8v, stream);
-  else dispatch_attn_main(a, kind, dp, mode, int8v, stream);
+  if (gen) {
+    if (dump) dispatch_attn_gen_dump(a, kind, dp, mode, int8v, stream);
+    else if (bias) dispatch_attn_gen_bias(a, kind, dp, mode, int8v, stream);
+    else dispatch_attn_gen_main(a, kind, dp, mode, int8v, stream);
+  } else if (dump) {
+    dispatch_attn_dump(a, kind, dp, mode, int8v, stream);
+  } else if (bias) {
+    dispatch_attn_bias(a, kind, dp, mode, int8v, stream);
+  } else {
+    dispatch_attn_main(a, kind, dp, mode, int8v, stream);
+  }
 }
 
 }  // namespace tmx

@@ -37,7 +37,8 @@ struct AttnKArgs {
   float qk_scale;
   int hq, hk, group, d;
   int m_blocks;   // ceil(max_seqlen_q / rows per workgroup)
-  int mask_tiles; // block_n_mask / block_n
+  int mask_tiles; // 64-key tiles per routing block: block_n_mask / 64
+  int ng;         // 64-key tiles per online-softmax step: block_n / 64 (GEN kernels)
   int blkq, blkk;
   int causal;
   int q_fused;      // Q quantised in the attention kernel (128-row workgroups, BLKQ == 128)
@@ -245,8 +246,9 @@ enum AttnKind : int {
   kAttn16 = 2,       // 16-row kernel, one 64-row routing block per workgroup
 };
 
-// Launch one instantiation (defined in attn_inst_*.hip).
-void dispatch_attn(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, bool dump, bool bias,
+// Launch one instantiation (defined in attn_inst_*.hip).  gen selects the
+// GEN kernels (block_n > 64, or scale blocks that are not multiples of 64).
+void dispatch_attn(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, bool dump, bool bias, bool gen,
                    hipStream_t stream);
 
 }  // namespace tmx

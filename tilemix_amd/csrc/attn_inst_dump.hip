@@ -4,7 +4,7 @@
 namespace tmx {
 
 void dispatch_attn_dump(const AttnKArgs& a, int kind, int dp, int mode, bool int8v, hipStream_t stream) {
-  AttnLauncher<true, false>::run(a, kind, dp, mode, int8v, stream);
+  AttnLauncher<true, false, false>::run(a, kind, dp, mode, int8v, stream);
 }
 
 }  // namespace tmx

@@ -49,11 +49,14 @@
 namespace tmx {
 
 // Occupancy target: 4 waves per SIMD at head_dim 64; at 128 the LDS allows 2.
-template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS>
+template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS, bool GEN>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu(DP <= 64 ? 4 : 2, DP <= 64 ? 4 : 2)))
 attn16_kernel(const AttnKArgs a) {
   constexpr int BM = NW * 16;
+  // K/V scales per tile and lane: one, or (GEN) one per 4-key group kb of the
+  // lane's keys 16 kb + 4 lg .. + 3.
+  constexpr int NSG = GEN ? 4 : 1;
   constexpr int KS16 = DP / 32;  // fp16 k-steps (16x16x32)
   constexpr int KS8 = DP / 64;   // int8 k-steps (16x16x64)
   constexpr int NDB = DP / 16;   // 16-wide d blocks of O^T
@@ -150,16 +153,21 @@ attn16_kernel(const AttnKArgs a) {
     if (MODE == TILEMIX_ROUTING_INT8) return 1;
     return (int)((bits >> (unsigned)(n / a.mask_tiles)) & 1ull);
   };
-  // K (and int8 V) scale of tile n (reference :380-388: clamped block
-  // index), fp16, fetched with the tile's copy.
-  auto load_scale = [&](const f16* sc, const int32_t* cus, int n) -> f16 {
-    f16 s = (f16)1.0f;
+  // K (and int8 V) scales of tile n (reference :380-390: clamped block
+  // index of each key), fp16, fetched with the tile's copy: one per tile, or
+  // (GEN) one per 4-key group of the lane, exact for BLKK divisible by 4.
+  auto load_scales = [&](const f16* sc, const int32_t* cus, int n, f16 (&out)[NSG]) {
     const int base = cus[z], end = cus[z + 1];
-    if (end > base) {
-      const int idx = min(base + (n * kBN) / a.blkk, end - 1);
-      s = sc[(int64_t)idx * a.hk + hk];
+#pragma unroll
+    for (int kb = 0; kb < NSG; ++kb) {
+      f16 s = (f16)1.0f;
+      if (end > base) {
+        const int key = n * kBN + (GEN ? 16 * kb + 4 * lg : 0);
+        const int idx = min(base + key / a.blkk, end - 1);
+        s = sc[(int64_t)idx * a.hk + hk];
+      }
+      out[kb] = s;
     }
-    return s;
   };
 
   // ---- asynchronous tile loads (HBM -> LDS, no registers) -----------------
@@ -191,7 +199,8 @@ attn16_kernel(const AttnKArgs a) {
   // Copies are issued from inline assembly (async_load16_asm): the loop
   // orders them against its LDS reads itself (s_waitcnt + barrier per tile).
   const uint32_t smem_lds = lds_addr(smem);
-  auto issue_tile = [&](int n, int route, uint32_t stage) {
+  // with_v = false (a GEN max pass) copies the K tile only.
+  auto issue_tile = [&](int n, int route, uint32_t stage, bool with_v) {
     const int key0 = n * kBN;
     const int rem = Lk - key0;  // >= 1
     if (route == 0) {
@@ -210,7 +219,8 @@ attn16_kernel(const AttnKArgs a) {
       }
     }
     const uint32_t vstage = stage + KBUF;
-    if (!INT8V || route == 0) {
+    if (!with_v) {
+    } else if (!INT8V || route == 0) {
       const SRsrc rs = make_srsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
 #pragma unroll
       for (int i = 0; i < K16_I; ++i) {
@@ -262,43 +272,46 @@ attn16_kernel(const AttnKArgs a) {
   for (int db = 0; db < NDB; ++db) acc[db] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   int route_next = 0;
-  f16 sk_next = (f16)1.0f, sv_next = (f16)1.0f;
-  auto fetch_scales = [&](int n) {
+  f16 sk_next[NSG], sv_next[NSG];
+#pragma unroll
+  for (int kb = 0; kb < NSG; ++kb) sk_next[kb] = sv_next[kb] = (f16)1.0f;
+  // Route, scales and copies of tile n (with_v: also its V tile).
+  auto fetch_issue = [&](int n, uint32_t stage, bool with_v) {
+    route_next = route_of(n);
     if (MODE != TILEMIX_ROUTING_FP16 && route_next == 1) {
-      sk_next = load_scale(a.sk, a.cu_ks, n);
-      if (INT8V) sv_next = load_scale(a.sv, a.cu_vs, n);
+      load_scales(a.sk, a.cu_ks, n, sk_next);
+      if (INT8V && with_v) load_scales(a.sv, a.cu_vs, n, sv_next);
     }
+    issue_tile(n, route_next, stage, with_v);
   };
+
+  // ---- GEN: steps over (tile, pass) ---------------------------------------
+  // Group gs .. ge-1 of ng consecutive 64-key tiles is one block_n tile; with
+  // more than one tile it is visited twice (pass 0: max, pass 1: update),
+  // else once (pass 1).  The sequence ends when n reaches n_blocks.
+  const int ng = GEN ? a.ng : 1;
+  struct Step {
+    int n, pass, gs, ge;
+  };
+  auto first_step = [&]() -> Step {
+    const int ge = min(ng, n_blocks);
+    return Step{0, ge > 1 ? 0 : 1, 0, ge};
+  };
+  auto next_step = [&](const Step& s) -> Step {
+    if (s.n + 1 < s.ge) return Step{s.n + 1, s.pass, s.gs, s.ge};
+    if (s.pass == 0) return Step{s.gs, 1, s.gs, s.ge};
+    const int ge = min(s.ge + ng, n_blocks);
+    return Step{s.ge, ge - s.ge > 1 ? 0 : 1, s.ge, ge};
+  };
+
   if (n_blocks > 0) {
-    route_next = route_of(0);
-    fetch_scales(0);
-    issue_tile(0, route_next, smem_lds);
+    if constexpr (GEN) fetch_issue(0, smem_lds, first_step().pass == 1);
+    else fetch_issue(0, smem_lds, true);
   }
 
-  for (int n = 0; n < n_blocks; ++n) {
-    const int route = route_next;
-    const f16 sk16 = sk_next;
-    const f16 sv16 = sv_next;
-    unsigned char* stage = smem + (n & 1) * STAGE;
-    // Tile n has landed (own loads), then every wave's loads have landed and
-    // every wave is done with the other stage (tile n-1).
-    __builtin_amdgcn_s_waitcnt(0);
-    if (INT8V && route == 1) widen_v8(stage);
-    __syncthreads();
-    if (n + 1 < n_blocks) {
-      route_next = route_of(n + 1);
-      fetch_scales(n + 1);
-      issue_tile(n + 1, route_next, smem_lds + ((n + 1) & 1) * STAGE);
-    }
-
-    const int key0 = n * kBN;
-    // Fully masked for this wave (or rows past the sequence end): the
-    // reference's update is then an exact no-op (p = 0, alpha = 1).
-    const bool wave_skip = (row0w >= Lq) || (a.causal && key0 > row0w + 15 + diag);
-    if (wave_skip) continue;
-
-    // ---- S^T = K . Q^T, rounded to fp16 (packed pairs r, r+1) ----------
-    uint32_t s16[4][2];
+  // ---- S^T = K . Q^T of a staged tile, rounded to fp16 (packed pairs r, r+1)
+  auto tile_scores = [&](const unsigned char* stage, int route, const f16 (&skc)[NSG], int key0,
+                         uint32_t (&s16)[4][2]) {
     if (route == 0) {
       f32x4 c[4];
 #pragma unroll
@@ -329,14 +342,18 @@ attn16_kernel(const AttnKArgs a) {
         s16[kb][1] = pack_h2(c[kb][2], c[kb][3]);
       }
     } else {
-      const f16 sqk = sq16 * sk16;
-      const float ss = (float)(f16)fp32_round((float)sqk * a.qk_scale);
       // acc is accumulated on top of the integer bits of 1.5*2^23, so
       // float(bits) = 1.5*2^23 + acc exactly (|acc| < 2^22); fma(F, ss,
       // -1.5*2^23*ss) is then the single rounding of acc*ss (1.5*2^23*ss is
       // exact: ss has 11 significant bits).
       constexpr float kMagic = 12582912.0f;
-      const float negms = -kMagic * ss;
+      float ss[NSG], negms[NSG];
+#pragma unroll
+      for (int kb = 0; kb < NSG; ++kb) {
+        const f16 sqk = sq16 * skc[kb];
+        ss[kb] = (float)(f16)fp32_round((float)sqk * a.qk_scale);
+        negms[kb] = -kMagic * ss[kb];
+      }
       const i32x4 magic = {0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
       i32x4 c[4];
 #pragma unroll
@@ -360,10 +377,11 @@ attn16_kernel(const AttnKArgs a) {
       }
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        s16[kb][0] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[kb][0]), ss, negms)),
-                             fp32_round(__builtin_fmaf(__int_as_float(c[kb][1]), ss, negms)));
-        s16[kb][1] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[kb][2]), ss, negms)),
-                             fp32_round(__builtin_fmaf(__int_as_float(c[kb][3]), ss, negms)));
+        const int g = GEN ? kb : 0;
+        s16[kb][0] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[kb][0]), ss[g], negms[g])),
+                             fp32_round(__builtin_fmaf(__int_as_float(c[kb][1]), ss[g], negms[g])));
+        s16[kb][1] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[kb][2]), ss[g], negms[g])),
+                             fp32_round(__builtin_fmaf(__int_as_float(c[kb][3]), ss[g], negms[g])));
       }
     }
     if (DUMP && a.dump_f16 != nullptr && row_ok) {
@@ -377,8 +395,10 @@ attn16_kernel(const AttnKArgs a) {
             a.dump_f16[(int64_t)(q_start + row) * a.dump_t + (int64_t)h * a.dump_h + key] = pr[r & 1];
         }
     }
+  };
 
-    // ---- mask + optional bias ------------------------------------------
+  // ---- mask + optional bias ------------------------------------------------
+  auto tile_mask = [&](int key0, uint32_t (&s16)[4][2]) {
     const bool need_mask = (key0 + kBN > Lk) || (a.causal && key0 + kBN - 1 > row0w + diag);
     if (need_mask || BIAS) {
       const int lim = a.causal ? min(Lk - 1, row + diag) : Lk - 1;  // last valid key
@@ -404,21 +424,26 @@ attn16_kernel(const AttnKArgs a) {
           s16[kb][j] = __builtin_bit_cast(uint32_t, pr);
         }
     }
+  };
 
-    // ---- online softmax (reference _softmax_prefix_update) -------------
+  // ---- the row maximum of a tile (the row's 4 lanes) -----------------------
+  auto tile_max = [&](const uint32_t (&s16)[4][2]) -> float {
     uint32_t mx2 = pk_max(pk_max(pk_max(s16[0][0], s16[0][1]), pk_max(s16[1][0], s16[1][1])),
                           pk_max(pk_max(s16[2][0], s16[2][1]), pk_max(s16[3][0], s16[3][1])));
     const f16x2 mxh = __builtin_bit_cast(f16x2, mx2);
     float mx = fmaxf((float)mxh[0], (float)mxh[1]);
-    {
-      const float2 p1 = pair16(mx);
-      mx = fmaxf(p1.x, p1.y);
-      const float2 p2 = pair32(mx);
-      mx = fmaxf(p2.x, p2.y);
-    }
-    const bool has = mx != -INFINITY;
-    const float m_next = has ? fmaxf(m_i, mx) : m_i;
-    const float alpha = has ? fast_exp2(m_i - m_next) : 1.0f;
+    const float2 p1 = pair16(mx);
+    mx = fmaxf(p1.x, p1.y);
+    const float2 p2 = pair32(mx);
+    return fmaxf(p2.x, p2.y);
+  };
+
+  // ---- online softmax update (reference _softmax_prefix_update) ------------
+  // m_next is the row's new maximum, alpha = exp2(m_i - m_next) (1 if the
+  // step brings no valid key); p = fp16(exp2(s - m_next)), l and O are
+  // rescaled by alpha, O^T += V^T . P^T.  svc: the tile's V scales (int8 V).
+  auto tile_update = [&](const unsigned char* stage, int route, const f16 (&svc)[NSG],
+                         const uint32_t (&s16)[4][2], float m_next, float alpha) {
     // With no valid key yet the tile is all -inf and p must be 0: subtract 0.
     const float negm = m_next == -INFINITY ? 0.0f : -m_next;
     uint32_t p16[4][2];
@@ -447,12 +472,14 @@ attn16_kernel(const AttnKArgs a) {
     if (INT8V && route == 1) {
       // Reference :449-497: PV on int8 V codes with p scaled by the V block
       // scale in fp16: p_scaled = fp16(p * sv) (l keeps the unscaled p).
-      const f16x2 sv2 = {sv16, sv16};
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb)
+      for (int kb = 0; kb < 4; ++kb) {
+        const f16 s = svc[GEN ? kb : 0];
+        const f16x2 sv2 = {s, s};
 #pragma unroll
         for (int j = 0; j < 2; ++j)
           p16[kb][j] = __builtin_bit_cast(uint32_t, __builtin_bit_cast(f16x2, p16[kb][j]) * sv2);
+      }
     }
 
     // ---- O^T += V^T . P^T ----------------------------------------------
@@ -488,6 +515,79 @@ attn16_kernel(const AttnKArgs a) {
         }
         acc[db] = __builtin_amdgcn_mfma_f32_16x16x32_f16(av, pb, acc[db], 0, 0, 0);
       }
+    }
+  };
+
+  // Tiles fully masked for this wave (or rows past the sequence end): the
+  // reference's update is then an exact no-op (p = 0, alpha = 1), in either
+  // pass of a GEN step.
+  auto wave_skip = [&](int key0) { return (row0w >= Lq) || (a.causal && key0 > row0w + 15 + diag); };
+  if constexpr (!GEN) {
+    for (int n = 0; n < n_blocks; ++n) {
+      const int route = route_next;
+      const f16 skc[NSG] = {sk_next[0]};
+      const f16 svc[NSG] = {sv_next[0]};
+      unsigned char* stage = smem + (n & 1) * STAGE;
+      // Tile n has landed (own loads), then every wave's loads have landed and
+      // every wave is done with the other stage (tile n-1).
+      __builtin_amdgcn_s_waitcnt(0);
+      if (INT8V && route == 1) widen_v8(stage);
+      __syncthreads();
+      if (n + 1 < n_blocks) fetch_issue(n + 1, smem_lds + ((n + 1) & 1) * STAGE, true);
+
+      const int key0 = n * kBN;
+      if (wave_skip(key0)) continue;
+      uint32_t s16[4][2];
+      tile_scores(stage, route, skc, key0, s16);
+      tile_mask(key0, s16);
+      const float mx = tile_max(s16);
+      const bool has = mx != -INFINITY;
+      const float m_next = has ? fmaxf(m_i, mx) : m_i;
+      const float alpha = has ? fast_exp2(m_i - m_next) : 1.0f;
+      tile_update(stage, route, svc, s16, m_next, alpha);
+    }
+  } else {
+    float gmx = -INFINITY;  // row maximum of the current group's max pass
+    Step cur = first_step();
+    for (int si = 0; cur.n < n_blocks; ++si) {
+      const Step nxt = next_step(cur);
+      const int route = route_next;
+      f16 skc[NSG], svc[NSG];
+#pragma unroll
+      for (int kb = 0; kb < NSG; ++kb) {
+        skc[kb] = sk_next[kb];
+        svc[kb] = sv_next[kb];
+      }
+      unsigned char* stage = smem + (si & 1) * STAGE;
+      __builtin_amdgcn_s_waitcnt(0);
+      if (INT8V && route == 1 && cur.pass == 1) widen_v8(stage);
+      __syncthreads();
+      if (nxt.n < n_blocks) fetch_issue(nxt.n, smem_lds + ((si + 1) & 1) * STAGE, nxt.pass == 1);
+
+      const int key0 = cur.n * kBN;
+      if (!wave_skip(key0)) {
+        uint32_t s16[4][2];
+        tile_scores(stage, route, skc, key0, s16);
+        tile_mask(key0, s16);
+        const float mx = tile_max(s16);
+        if (cur.pass == 0) {
+          gmx = fmaxf(gmx, mx);
+        } else {
+          // The group's maximum enters at its first tile (alpha once per
+          // block_n tile); later tiles of the group keep m (alpha = 1).
+          float m_next = m_i, alpha = 1.0f;
+          if (cur.n == cur.gs) {
+            const float gm = fmaxf(gmx, mx);
+            gmx = -INFINITY;
+            if (gm != -INFINITY) {
+              m_next = fmaxf(m_i, gm);
+              alpha = fast_exp2(m_i - m_next);
+            }
+          }
+          tile_update(stage, route, svc, s16, m_next, alpha);
+        }
+      }
+      cur = nxt;
     }
   }
 

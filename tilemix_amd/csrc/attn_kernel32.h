@@ -17,6 +17,18 @@
 // Tiles are visited in ascending key order; tile n uses route bit
 // (bitmask[hk*ceil(Lq/block_m)+m] >> (n / (block_n_mask/64))) & 1        (:818-933).
 //
+// The kernel computes in 64-key tiles.  GEN instantiations serve the other
+// launch shapes of the reference:
+//   * block_n = 64 * ng (ng = 2, 4): the reference's online-softmax step covers
+//     block_n keys, m' = max(m, max over the block_n keys) and p = fp16(exp2(s
+//     - m')) (:179-207).  Each block_n tile is streamed twice, 64 keys at a
+//     time: a max pass (K only: scores, mask, row maximum) and an update pass
+//     (scores again, p against that maximum, one rescale per block_n tile, PV);
+//   * K/V scale blocks (BLKK) that are not multiples of 64: the scale is
+//     looked up per 4-key group of a lane, sk[key // BLKK] (:390,485), which is
+//     exact for every BLKK divisible by 4 (no scale block starts inside a
+//     4-aligned group of keys).
+//
 // Work decomposition (MI355X-first, not the reference's):
 //   * one workgroup = one (sequence, query head, block_m query rows);
 //     NW = block_m/32 waves, each wave owns 32 query rows;
@@ -42,11 +54,14 @@
 
 namespace tmx {
 
-template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS, bool SPLIT>
+template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS, bool SPLIT, bool GEN>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn32_kernel(const AttnKArgs a) {
   static_assert(!SPLIT || (NW % 2 == 0 && !INT8V), "split workgroups: even wave count, fp16 V");
   constexpr int BM = NW * 32;
+  // K/V scales per tile and lane: one, or (GEN) one per 4-key group g = 4 kb + jj
+  // of the lane's keys 32 kb + 8 jj + 4 hi .. + 3.
+  constexpr int NSG = GEN ? 8 : 1;
   constexpr int KS16 = DP / 16;  // fp16 MFMA k-steps (32x32x16)
   constexpr int KS8 = DP / 32;   // int8 MFMA k-steps (32x32x32)
   constexpr int NDB = DP / 32;   // 32-wide d blocks of O^T
@@ -176,7 +191,8 @@ attn32_kernel(const AttnKArgs a) {
   const unsigned char* v8cur = v8seq;
   int kleft = (int)(Lk * kt_bytes), k8left = (int)(Lk * k8t_bytes);
   int vleft = (int)(Lk * vt_bytes), v8left = (int)(Lk * v8t_bytes);
-  auto issue_tile = [&](int route, uint32_t stage) {
+  // with_v = false (a GEN max pass) copies the K tile only.
+  auto issue_tile = [&](int route, uint32_t stage, bool with_v) {
     const bool need16 = MODE != TILEMIX_ROUTING_INT8 && (SPLIT ? route != 3 : route == 0);
     const bool need8 = MODE != TILEMIX_ROUTING_FP16 && route != 0;
     if (need16) {
@@ -199,7 +215,8 @@ attn32_kernel(const AttnKArgs a) {
         async_load16_asm(rs, o + i * step_k8, stage + K8OFF + (i * NW + wave) * 1024);
     }
     const uint32_t vstage = stage + KBUF;
-    if (!INT8V || route == 0) {
+    if (!with_v) {
+    } else if (!INT8V || route == 0) {
       const SRsrc rs = make_srsrc(vcur, vleft);
       int o = dma_v16;
       asm volatile("" : "+v"(o));
@@ -259,36 +276,38 @@ attn32_kernel(const AttnKArgs a) {
   // reference's min(block, last) lookup), advanced by pointer.
   bool has_ks = false, has_vs = false;
   const f16 *skp = nullptr, *sk_last = nullptr, *svp = nullptr, *sv_last = nullptr;
+  int ks_base = 0, ks_end = 0, vs_base = 0, vs_end = 0;
   if (MODE != TILEMIX_ROUTING_FP16) {
-    const int kbase = a.cu_ks[z], kend = a.cu_ks[z + 1];
-    has_ks = kend > kbase;
-    skp = a.sk + (int64_t)kbase * a.hk + hk;
-    sk_last = a.sk + (int64_t)(kend - 1) * a.hk + hk;
+    ks_base = a.cu_ks[z];
+    ks_end = a.cu_ks[z + 1];
+    has_ks = ks_end > ks_base;
+    skp = a.sk + (int64_t)ks_base * a.hk + hk;
+    sk_last = a.sk + (int64_t)(ks_end - 1) * a.hk + hk;
   }
   if (INT8V) {
-    const int vbase = a.cu_vs[z], vend = a.cu_vs[z + 1];
-    has_vs = vend > vbase;
-    svp = a.sv + (int64_t)vbase * a.hk + hk;
-    sv_last = a.sv + (int64_t)(vend - 1) * a.hk + hk;
+    vs_base = a.cu_vs[z];
+    vs_end = a.cu_vs[z + 1];
+    has_vs = vs_end > vs_base;
+    svp = a.sv + (int64_t)vs_base * a.hk + hk;
+    sv_last = a.sv + (int64_t)(vs_end - 1) * a.hk + hk;
   }
+  // Route of tile nx in route group grp (0 fp16 / 1 int8; SPLIT: two bits).
+  auto tile_route = [&](int nx, int grp) -> int {
+    if (MODE == TILEMIX_ROUTING_FP16) return 0;
+    if (MODE == TILEMIX_ROUTING_INT8) return SPLIT ? 3 : 1;
+    if (!SPLIT) return (int)((bits >> (unsigned)grp) & 1ull);
+    const int rhi = (int)((bits_hi >> (unsigned)grp) & 1ull);
+    const int rlo = nx * kBN > lo_last_key ? rhi : (int)((bits >> (unsigned)grp) & 1ull);
+    return rlo | (rhi << 1);
+  };
   // Issues the next tile (index nx) and fetches its scales; the loads land
   // before the barrier that precedes the tile's compute.
-  auto issue_next = [&](int nx, uint32_t stage, int& route, f16& skv, f16& svv) {
-    if (MODE == TILEMIX_ROUTING_FP16) {
-      route = 0;
-    } else if (MODE == TILEMIX_ROUTING_INT8) {
-      route = SPLIT ? 3 : 1;
-    } else if (!SPLIT) {
-      route = (int)((bits >> (unsigned)nx_grp) & 1ull);
-    } else {
-      const int rhi = (int)((bits_hi >> (unsigned)nx_grp) & 1ull);
-      const int rlo = nx * kBN > lo_last_key ? rhi : (int)((bits >> (unsigned)nx_grp) & 1ull);
-      route = rlo | (rhi << 1);
-    }
-    issue_tile(route, stage);
+  auto issue_next = [&](int nx, uint32_t stage, int& route, f16 (&skv)[NSG], f16 (&svv)[NSG]) {
+    route = tile_route(nx, nx_grp);
+    issue_tile(route, stage, true);
     if (MODE != TILEMIX_ROUTING_FP16 && route != 0) {
-      skv = has_ks ? *skp : (f16)1.0f;
-      if (INT8V) svv = has_vs ? *svp : (f16)1.0f;
+      skv[0] = has_ks ? *skp : (f16)1.0f;
+      if (INT8V) svv[0] = has_vs ? *svp : (f16)1.0f;
     }
     if (++nx_gc == a.mask_tiles) {
       nx_gc = 0;
@@ -301,11 +320,68 @@ attn32_kernel(const AttnKArgs a) {
     }
   };
 
+  // ---- GEN: steps over (tile, pass) ---------------------------------------
+  // Group gs .. ge-1 of ng consecutive 64-key tiles is one block_n tile; with
+  // more than one tile it is visited twice (pass 0: max, pass 1: update),
+  // else once (pass 1).  The sequence ends when n reaches n_blocks.
+  const int ng = GEN ? a.ng : 1;
+  struct Step {
+    int n, pass, gs, ge;
+  };
+  auto first_step = [&]() -> Step {
+    const int ge = min(ng, n_blocks);
+    return Step{0, ge > 1 ? 0 : 1, 0, ge};
+  };
+  auto next_step = [&](const Step& s) -> Step {
+    if (s.n + 1 < s.ge) return Step{s.n + 1, s.pass, s.gs, s.ge};
+    if (s.pass == 0) return Step{s.gs, 1, s.gs, s.ge};
+    const int ge = min(s.ge + ng, n_blocks);
+    return Step{s.ge, ge - s.ge > 1 ? 0 : 1, s.ge, ge};
+  };
+  // Scale of each of this lane's 4-key groups of tile n (the reference's
+  // clamped per-key lookup, sk[min(base + key // BLKK, end - 1)]).
+  auto group_scales = [&](int n, const f16* sh, int base, int end, bool has, f16 (&out)[NSG]) {
+#pragma unroll
+    for (int g = 0; g < NSG; ++g) {
+      const unsigned key = (unsigned)(n * kBN + 32 * (g >> 2) + 8 * (g & 3) + 4 * hi);
+      const int idx = min(base + (int)(key / (unsigned)a.blkk), end - 1);
+      out[g] = has ? sh[(int64_t)idx * a.hk] : (f16)1.0f;
+    }
+  };
+  // Issues step s's tile: the stream bases are set from the tile index (the
+  // steps revisit tiles), and a max pass copies K only.
+  auto issue_step = [&](const Step& s, uint32_t stage, int& route, f16 (&skv)[NSG], f16 (&svv)[NSG]) {
+    route = tile_route(s.n, s.n / a.mask_tiles);
+    const int key0 = s.n * kBN;
+    kcur = kseq + (int64_t)key0 * kt_bytes;
+    kleft = (int)((Lk - key0) * kt_bytes);
+    vcur = vseq + (int64_t)key0 * vt_bytes;
+    vleft = (int)((Lk - key0) * vt_bytes);
+    if (MODE != TILEMIX_ROUTING_FP16) {
+      k8cur = k8seq + (int64_t)key0 * k8t_bytes;
+      k8left = (int)((Lk - key0) * k8t_bytes);
+    }
+    if (INT8V) {
+      v8cur = v8seq + (int64_t)key0 * v8t_bytes;
+      v8left = (int)((Lk - key0) * v8t_bytes);
+    }
+    issue_tile(route, stage, s.pass == 1);
+    if (MODE != TILEMIX_ROUTING_FP16 && route != 0) {
+      group_scales(s.n, a.sk + hk, ks_base, ks_end, has_ks, skv);
+      if (INT8V && s.pass == 1) group_scales(s.n, a.sv + hk, vs_base, vs_end, has_vs, svv);
+    }
+  };
+
   // The first tile's copies go out before Q is loaded, so the two
   // latencies overlap.
   int route_next = 0;
-  f16 sk_next = (f16)1.0f, sv_next = (f16)1.0f;
-  if (n_blocks > 0) issue_next(0, smem_lds, route_next, sk_next, sv_next);
+  f16 sk_next[NSG], sv_next[NSG];
+#pragma unroll
+  for (int g = 0; g < NSG; ++g) sk_next[g] = sv_next[g] = (f16)1.0f;
+  if (n_blocks > 0) {
+    if constexpr (GEN) issue_step(first_step(), smem_lds, route_next, sk_next, sv_next);
+    else issue_next(0, smem_lds, route_next, sk_next, sv_next);
+  }
 
   // ---- Q fragments (B operand of S^T = K . Q^T) --------------------------
   // Lane (row, hi) holds Q[row][16 s + 8 hi .. + 7] for the fp16 k-steps s and
@@ -432,6 +508,14 @@ attn32_kernel(const AttnKArgs a) {
     if (n + 1 < n_blocks)
       issue_next(n + 1, smem_lds + ((n + 1) & 1) * STAGE, route_next, sk_next, sv_next);
   };
+  // GEN: the same for step cur (stage si & 1), issuing step nxt.
+  auto step_start = [&](int si, const Step& cur, const Step& nxt) {
+    const int route = SPLIT ? (route_next >> half) & 1 : route_next;
+    __builtin_amdgcn_s_waitcnt(0);
+    if (INT8V && route == 1 && cur.pass == 1) widen_v8(smem + (si & 1) * STAGE);
+    __syncthreads();
+    if (nxt.n < n_blocks) issue_step(nxt, smem_lds + ((si + 1) & 1) * STAGE, route_next, sk_next, sv_next);
+  };
   // Tiles [n_wave, n_blocks) are fully masked for this wave's rows (causal),
   // or the wave's rows lie past the sequence end: the reference's update is
   // then an exact no-op (p = 0, alpha = 1), so the wave only keeps the
@@ -441,16 +525,10 @@ attn32_kernel(const AttnKArgs a) {
   int n_wave = n_blocks;
   if (row0w >= Lq) n_wave = 0;
   else if (a.causal) n_wave = min(n_blocks, row0w + 31 + diag < 0 ? 0 : (row0w + 31 + diag) / kBN + 1);
-  for (int n = 0; n < n_wave; ++n) {
-    const int route = SPLIT ? (route_next >> half) & 1 : route_next;
-    const f16 sk16 = sk_next;
-    const f16 sv16 = sv_next;
-    unsigned char* stage = smem + (n & 1) * STAGE;
-    tile_start(n);
-    const int key0 = n * kBN;
 
-    // ---- S^T = K . Q^T, rounded to fp16 (packed pairs r, r+1) ----------
-    uint32_t s16[2][8];
+  // ---- S^T = K . Q^T of a staged tile, rounded to fp16 (packed pairs r, r+1)
+  auto tile_scores = [&](const unsigned char* stage, int route, const f16 (&skc)[NSG], int key0,
+                         uint32_t (&s16)[2][8]) {
     if (route == 0) {
       int kbase16 = l32 * ROW16 + ((16 * hi) ^ (16 * swz_k<ROW16>(l32)));
       asm volatile("" : "+v"(kbase16));
@@ -476,16 +554,20 @@ attn32_kernel(const AttnKArgs a) {
         for (int j = 0; j < 8; ++j) s16[kb][j] = pack_h2(c[2 * j], c[2 * j + 1]);
       }
     } else {
-      const f16 sqk = sq16 * sk16;
       // ss is fp16-exact; the barrier keeps it an fp32 operand (v_fma_f32
       // below, not the slower mixed-precision form).
-      const float ss = fp32_round((float)(f16)fp32_round((float)sqk * a.qk_scale));
       // acc is accumulated on top of the integer bits of 1.5*2^23, so
       // float(bits) = 1.5*2^23 + acc exactly (|acc| < 2^22); fma(F, ss,
       // -1.5*2^23*ss) is then the single rounding of acc*ss (1.5*2^23*ss is
       // exact: ss has 11 significant bits).
       constexpr float kMagic = 12582912.0f;
-      const float negms = -kMagic * ss;
+      float ss[NSG], negms[NSG];
+#pragma unroll
+      for (int g = 0; g < NSG; ++g) {
+        const f16 sqk = sq16 * skc[g];
+        ss[g] = fp32_round((float)(f16)fp32_round((float)sqk * a.qk_scale));
+        negms[g] = -kMagic * ss[g];
+      }
       int kbase8 = l32 * ROW8 + ((16 * hi) ^ (16 * swz_k<ROW8>(l32)));
       asm volatile("" : "+v"(kbase8));
       // Chain kb = 0 first; its dequant FMAs then run while the MFMAs of
@@ -511,9 +593,11 @@ attn32_kernel(const AttnKArgs a) {
           }
         }
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-          s16[kb][j] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[2 * j] + kBiasAdd), ss, negms)),
-                               fp32_round(__builtin_fmaf(__int_as_float(c[2 * j + 1] + kBiasAdd), ss, negms)));
+        for (int j = 0; j < 8; ++j) {
+          const int g = GEN ? 4 * kb + (j >> 1) : 0;  // keys 2 j, 2 j + 1 of the lane's 16 in kb
+          s16[kb][j] = pack_h2(fp32_round(__builtin_fmaf(__int_as_float(c[2 * j] + kBiasAdd), ss[g], negms[g])),
+                               fp32_round(__builtin_fmaf(__int_as_float(c[2 * j + 1] + kBiasAdd), ss[g], negms[g])));
+        }
       };
       const i32x16 c0 = qk8_chain(0);
       __builtin_amdgcn_sched_barrier(0);
@@ -533,8 +617,10 @@ attn32_kernel(const AttnKArgs a) {
             a.dump_f16[(int64_t)(q_start + row) * a.dump_t + (int64_t)h * a.dump_h + key] = pr[rr & 1];
         }
     }
+  };
 
-    // ---- mask + optional bias ------------------------------------------
+  // ---- mask + optional bias ------------------------------------------------
+  auto tile_mask = [&](int key0, uint32_t (&s16)[2][8]) {
     const bool need_mask = (key0 + kBN > Lk) || (a.causal && key0 + kBN - 1 > row0w + diag);
     if (need_mask || BIAS) {
       const int lim = a.causal ? min(Lk - 1, row + diag) : Lk - 1;  // last valid key
@@ -561,21 +647,26 @@ attn32_kernel(const AttnKArgs a) {
           s16[kb][j] = __builtin_bit_cast(uint32_t, pr);
         }
     }
+  };
 
-    // ---- online softmax (reference _softmax_prefix_update) -------------
+  // ---- the row maximum of a tile (both lanes of the row) -------------------
+  auto tile_max = [&](const uint32_t (&s16)[2][8]) -> float {
     // 16 packed pairs -> 1 in 8 three-input maxima.
     const uint32_t u0 = pk_max3(s16[0][0], s16[0][1], s16[0][2]), u1 = pk_max3(s16[0][3], s16[0][4], s16[0][5]);
     const uint32_t u2 = pk_max3(s16[0][6], s16[0][7], s16[1][0]), u3 = pk_max3(s16[1][1], s16[1][2], s16[1][3]);
     const uint32_t u4 = pk_max3(s16[1][4], s16[1][5], s16[1][6]);
     const f16x2 mx2 = __builtin_bit_cast(f16x2, pk_max(pk_max3(u0, u1, u2), pk_max3(u3, u4, s16[1][7])));
-    float mx = fmaxf((float)mx2[0], (float)mx2[1]);
-    {
-      const float2 sw = swap_halves(mx);
-      mx = fmaxf(sw.x, sw.y);
-    }
-    const bool has = mx != -INFINITY;
-    const float m_next = has ? fmaxf(m_i, mx) : m_i;
-    const float alpha = has ? fast_exp2(m_i - m_next) : 1.0f;
+    const float mx = fmaxf((float)mx2[0], (float)mx2[1]);
+    const float2 sw = swap_halves(mx);
+    return fmaxf(sw.x, sw.y);
+  };
+
+  // ---- online softmax update (reference _softmax_prefix_update) ------------
+  // m_next is the row's new maximum, alpha = exp2(m_i - m_next) (1 if the
+  // step brings no valid key); p = fp16(exp2(s - m_next)), l and O are
+  // rescaled by alpha, O^T += V^T . P^T.  svc: the tile's V scales (int8 V).
+  auto tile_update = [&](const unsigned char* stage, int route, const f16 (&svc)[NSG],
+                         const uint32_t (&s16)[2][8], float m_next, float alpha) {
     // With no valid key yet the tile is all -inf and p must be 0: subtract 0.
     const float negm = m_next == -INFINITY ? 0.0f : -m_next;
     // P^T as the B operands of the PV MFMAs: pv[ks] holds keys 16 ks .. 16 ks + 15
@@ -607,10 +698,14 @@ attn32_kernel(const AttnKArgs a) {
 
     if (INT8V && route == 1) {
       // Reference :449-497: PV on int8 V codes with p scaled by the V block
-      // scale in fp16: p_scaled = fp16(p * sv).
-      const f16x8 sv8 = {sv16, sv16, sv16, sv16, sv16, sv16, sv16, sv16};
+      // scale in fp16: p_scaled = fp16(p * sv).  GEN: elements 0-3 of pv[ks]
+      // are keys of the lane's group 2 ks, elements 4-7 of group 2 ks + 1.
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) pv[ks] = __builtin_bit_cast(u32x4, __builtin_bit_cast(f16x8, pv[ks]) * sv8);
+      for (int ks = 0; ks < 4; ++ks) {
+        const f16 s0 = svc[GEN ? 2 * ks : 0], s1 = svc[GEN ? 2 * ks + 1 : 0];
+        const f16x8 sv8 = {s0, s0, s0, s0, s1, s1, s1, s1};
+        pv[ks] = __builtin_bit_cast(u32x4, __builtin_bit_cast(f16x8, pv[ks]) * sv8);
+      }
     }
 
     // ---- O^T += V^T . P^T ----------------------------------------------
@@ -641,8 +736,68 @@ attn32_kernel(const AttnKArgs a) {
         acc[db] = __builtin_amdgcn_mfma_f32_32x32x16_f16(av, pb, acc[db], 0, 0, 0);
       }
     }
+  };
+
+  if constexpr (!GEN) {
+    for (int n = 0; n < n_wave; ++n) {
+      const int route = SPLIT ? (route_next >> half) & 1 : route_next;
+      const f16 skc[NSG] = {sk_next[0]};
+      const f16 svc[NSG] = {sv_next[0]};
+      unsigned char* stage = smem + (n & 1) * STAGE;
+      tile_start(n);
+      const int key0 = n * kBN;
+      uint32_t s16[2][8];
+      tile_scores(stage, route, skc, key0, s16);
+      tile_mask(key0, s16);
+      const float mx = tile_max(s16);
+      const bool has = mx != -INFINITY;
+      const float m_next = has ? fmaxf(m_i, mx) : m_i;
+      const float alpha = has ? fast_exp2(m_i - m_next) : 1.0f;
+      tile_update(stage, route, svc, s16, m_next, alpha);
+    }
+    for (int n = n_wave; n < n_blocks; ++n) tile_start(n);
+  } else {
+    // Steps of tiles n >= n_wave are no-ops for this wave (fully masked rows)
+    // in both passes: the wave keeps the barriers and copies going only.
+    float gmx = -INFINITY;  // row maximum of the current group's max pass
+    Step cur = first_step();
+    for (int si = 0; cur.n < n_blocks; ++si) {
+      const Step nxt = next_step(cur);
+      const int route = SPLIT ? (route_next >> half) & 1 : route_next;
+      f16 skc[NSG], svc[NSG];
+#pragma unroll
+      for (int g = 0; g < NSG; ++g) {
+        skc[g] = sk_next[g];
+        svc[g] = sv_next[g];
+      }
+      unsigned char* stage = smem + (si & 1) * STAGE;
+      step_start(si, cur, nxt);
+      if (cur.n < n_wave) {
+        const int key0 = cur.n * kBN;
+        uint32_t s16[2][8];
+        tile_scores(stage, route, skc, key0, s16);
+        tile_mask(key0, s16);
+        const float mx = tile_max(s16);
+        if (cur.pass == 0) {
+          gmx = fmaxf(gmx, mx);
+        } else {
+          // The group's maximum enters at its first tile (alpha once per
+          // block_n tile); later tiles of the group keep m (alpha = 1).
+          float m_next = m_i, alpha = 1.0f;
+          if (cur.n == cur.gs) {
+            const float gm = fmaxf(gmx, mx);
+            gmx = -INFINITY;
+            if (gm != -INFINITY) {
+              m_next = fmaxf(m_i, gm);
+              alpha = fast_exp2(m_i - m_next);
+            }
+          }
+          tile_update(stage, route, svc, s16, m_next, alpha);
+        }
+      }
+      cur = nxt;
+    }
   }
-  for (int n = n_wave; n < n_blocks; ++n) tile_start(n);
 
   // ---- epilogue: out = fp16(acc / l) --------------------------------------
   {

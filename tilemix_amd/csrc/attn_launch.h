@@ -7,24 +7,24 @@
 
 namespace tmx {
 
-template <bool DUMP, bool BIAS>
+template <bool DUMP, bool BIAS, bool GEN>
 struct AttnLauncher {
   template <int DP, int MODE, bool INT8V>
   static void one(const AttnKArgs& a, int kind, hipStream_t stream) {
     const dim3 grid(8 * a.per_xcd), block(256);
     if constexpr (MODE == TILEMIX_ROUTING_MIXED && INT8V) {
       if (kind == kAttn16) {
-        hipLaunchKernelGGL((attn16_kernel<4, DP, MODE, INT8V, DUMP, BIAS>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn16_kernel<4, DP, MODE, INT8V, DUMP, BIAS, GEN>), grid, block, 0, stream, a);
         return;
       }
     }
     if constexpr (MODE == TILEMIX_ROUTING_MIXED && !INT8V) {
       if (kind == kAttn32Split) {
-        hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, true>), grid, block, 0, stream, a);
+        hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, true, GEN>), grid, block, 0, stream, a);
         return;
       }
     }
-    hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, false, GEN>), grid, block, 0, stream, a);
   }
 
   template <int DP>
