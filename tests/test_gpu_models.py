@@ -35,7 +35,8 @@ def _oracle_varlen_attention(q, k, v, block_m, block_n, *, block_n_mask=None, ca
     bits = np.array([int(x) for x in precision_map_all.reshape(-1).tolist()], dtype=np.uint64)
     out = O.attn_fwd(qn, kn, vn, cu, cu, bits, block_m=block_m, block_n_mask=block_n_mask or block_n,
                      causal=causal, sm_scale=scale, q8=q8, k8=k8, sq16=sq.astype(np.float16),
-                     sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk, fp16_accum=fp16_accum)
+                     sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk, fp16_accum=fp16_accum,
+                     block_n=block_n)
     o = torch.from_numpy(out.astype(np.float32)).to(q.device, torch.float16)
     return o.view(B, T, Hq, D).permute(0, 2, 1, 3)
 
@@ -61,6 +62,53 @@ def test_llama_tilemix_matches_oracle_attention(device, monkeypatch):
     TL.configure_tilemix_attention_pattern(model, "sptrans", percentage=0.5, stride=128, c=32)
     g = torch.Generator().manual_seed(1)
     ids = torch.randint(0, 512, (4, 384), generator=g).to(device)
+    agree, dmax, dmean = _compare(model, TL, ids, monkeypatch)
+    assert agree >= 0.999, agree
+    assert dmax < 0.05 and dmean < 2e-3, (dmax, dmean)
+
+
+@pytest.mark.parametrize("forced", ["64,128", "64,256"])
+def test_llama_forced_block_n(device, monkeypatch, forced):
+    """TILEMIX_FORCE_CONFIG picks the reference's (64, 128) / (64, 256) sizes
+    (models/tilemix_llama.py:143-153): the model runs the block_n > 64 kernels
+    and agrees with the oracle attention of the same block_n."""
+    monkeypatch.setenv("TILEMIX_FORCE_CONFIG", forced)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, rope_theta=500000.0)
+    torch.manual_seed(7)
+    model = LlamaForCausalLM(cfg).half().to(device).eval()
+    TL.inject_tilemix_into_llama(model)
+    TL.configure_tilemix_attention_pattern(model, "sptrans", percentage=0.5, stride=128, c=32)
+    seen = []
+    real = TL.tilemix_varlen_attention
+
+    def spy(q, k, v, block_m, block_n, **kw):
+        seen.append((block_m, block_n))
+        return real(q, k, v, block_m, block_n, **kw)
+
+    ids = torch.randint(0, 512, (2, 640), generator=torch.Generator().manual_seed(8)).to(device)
+    with torch.no_grad():
+        monkeypatch.setattr(TL, "tilemix_varlen_attention", spy)
+        got = model(ids).logits.float()
+        monkeypatch.setattr(TL, "tilemix_varlen_attention", _oracle_varlen_attention)
+        ref = model(ids).logits.float()
+    assert set(seen) == {tuple(int(x) for x in forced.split(","))}
+    agree = (got.argmax(-1) == ref.argmax(-1)).float().mean().item()
+    diff = (got - ref).abs()
+    assert agree >= 0.999, agree
+    assert diff.max().item() < 0.05 and diff.mean().item() < 2e-3
+
+
+def test_llama_head_dim_72(device, monkeypatch):
+    """A head_dim that is not a multiple of 16 (72): the host zero-pads Q/K/V
+    and the model agrees with the oracle attention at the original width."""
+    cfg = LlamaConfig(vocab_size=512, hidden_size=288, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, head_dim=72)
+    torch.manual_seed(9)
+    model = LlamaForCausalLM(cfg).half().to(device).eval()
+    TL.inject_tilemix_into_llama(model)
+    TL.configure_tilemix_attention_pattern(model, "sptrans", percentage=0.5, stride=128, c=32)
+    ids = torch.randint(0, 512, (2, 320), generator=torch.Generator().manual_seed(10)).to(device)
     agree, dmax, dmean = _compare(model, TL, ids, monkeypatch)
     assert agree >= 0.999, agree
     assert dmax < 0.05 and dmean < 2e-3, (dmax, dmean)
