@@ -163,3 +163,112 @@ def test_lds_receives_every_valid_chunk_once():
         seen[o // tok, (o % tok) // 16] += 1
     assert (seen[:, : 2 * d // 16] == 1).all()
     assert (seen[:, 2 * d // 16:] == 0).all()
+
+
+# ---------------------------------------------------------------- Q block copy
+def q_block_through_lds(q, cu, h, m, d, dp, read_swz_from_block_row=False, copy_swizzle=True):
+    """Model of the 32-row kernel's Q staging for query block m (128 rows) of
+    every sequence, head h: each wave w copies rows 32 w .. 32 w + 31 of the
+    block into LDS (K-tile layout, raw buffer based at the wave's first row,
+    sized to the rows left in the sequence), then lane (l32, hi) reads k-step s
+    at (row * ROW16 + ((16 hi) ^ (16 swz_k(l32)))) ^ (32 s).  Returns, per
+    sequence, the [128, DP] fp16 block as the lanes see it, and the relative
+    byte addresses every copy read.  ``read_swz_from_block_row`` swizzles the
+    read with the block row instead of the lane's (equivalent: the swizzle
+    depends on the row mod 16); ``copy_swizzle=False`` plants an unswizzled copy."""
+    row16 = 2 * dp
+    qrpi, qcpr = 1024 // row16, row16 // 16
+    qins = 32 // qrpi
+    ntok, hq, hstride = q.shape
+    tok = 2 * hstride * hq
+    raw = q.view(np.uint8).reshape(-1)
+    blocks, reads = [], []
+    for z in range(len(cu) - 1):
+        lq = int(cu[z + 1] - cu[z])
+        lds = np.full(128 * row16, 0xEE, dtype=np.uint8)
+        for w in range(4):
+            row0w = m * 128 + 32 * w
+            base = (int(cu[z]) + row0w) * tok + h * 2 * hstride
+            size = (lq - row0w) * tok if row0w < lq else 0
+            for i in range(qins):
+                for lane in range(64):
+                    rl = i * qrpi + lane // qcpr
+                    chunk = (lane % qcpr) ^ (swz_k(row16, w * 32 + rl) if copy_swizzle else 0)
+                    off = OUTSIDE if chunk * 16 >= 2 * d else rl * tok + chunk * 16
+                    dst = (w * 32 + i * qrpi) * row16 + lane * 16
+                    for dw in range(4):
+                        o = off + 4 * dw
+                        if o < size:
+                            reads.append(base + o + np.arange(4))
+                            lds[dst + 4 * dw:dst + 4 * dw + 4] = raw[base + o:base + o + 4]
+                        else:
+                            lds[dst + 4 * dw:dst + 4 * dw + 4] = 0
+        got = np.zeros((128, dp), dtype=np.float16)
+        for w in range(4):
+            for lane in range(64):
+                l32, hi = lane & 31, lane >> 5
+                r = w * 32 + l32
+                sw = swz_k(row16, r if read_swz_from_block_row else l32)
+                qbase = r * row16 + ((16 * hi) ^ (16 * sw))
+                for s in range(dp // 16):
+                    a = qbase ^ (32 * s)
+                    got[r, 16 * s + 8 * hi:16 * s + 8 * hi + 8] = lds[a:a + 16].view(np.float16)
+        blocks.append(got)
+    return blocks, (np.concatenate(reads) if reads else np.zeros(0, dtype=np.int64))
+
+
+# d, DP, Hq, head stride (elements), lengths, block m
+Q_CASES = [
+    (128, 128, 3, 128, [300, 129, 1], 0),
+    (128, 128, 3, 128, [300, 129, 1], 1),
+    (80, 128, 2, 128, [200, 37], 1),     # [..., :80] view of a 128-wide buffer
+    (80, 128, 2, 80, [140, 129], 1),
+    (48, 64, 3, 48, [100, 130], 0),
+    (64, 64, 2, 64, [257], 2),
+]
+
+
+@pytest.mark.parametrize("d,dp,hq,hstride,lens,m", Q_CASES)
+def test_q_block_staging(d, dp, hq, hstride, lens, m):
+    """Each lane receives exactly Q[row][16 s + 8 hi .. + 7] of its row (zeros
+    past the sequence end and past head_dim), and every byte the copies read
+    belongs to a valid element of the block's own head."""
+    rng = np.random.default_rng(d + m)
+    ntok = sum(lens)
+    q = np.full((ntok, hq, hstride), np.nan, dtype=np.float16)  # padding and other heads: NaN
+    q[:, :, :d] = rng.standard_normal((ntok, hq, d)).astype(np.float16)
+    cu = np.concatenate([[0], np.cumsum(lens)])
+    for h in range(hq):
+        blocks, addr = q_block_through_lds(q, cu, h, m, d, dp)
+        tok = 2 * hstride * hq
+        if addr.size:
+            head, col = (addr % tok) // (2 * hstride), (addr % (2 * hstride)) // 2
+            assert addr.max() < ntok * tok and (head == h).all() and (col < d).all()
+        for z, got in enumerate(blocks):
+            lq = int(cu[z + 1] - cu[z])
+            want = np.zeros((128, dp), dtype=np.float16)
+            rows = max(0, min(128, lq - m * 128))
+            want[:rows, :d] = q[cu[z] + m * 128:cu[z] + m * 128 + rows, h, :d]
+            np.testing.assert_array_equal(got.view(np.uint16), want.view(np.uint16))
+
+
+def test_q_block_read_swizzle_uses_the_lane_row():
+    """The fragment reads swizzle with the lane's row l32 rather than the block
+    row 32 w + l32: the same value for every wave (the swizzle depends on the
+    row mod 16), checked at both row widths."""
+    for dp in (64, 128):
+        q = np.random.default_rng(dp).standard_normal((256, 1, dp)).astype(np.float16)
+        cu = np.array([0, 256])
+        got, _ = q_block_through_lds(q, cu, 0, 0, dp, dp, read_swz_from_block_row=True)
+        ok, _ = q_block_through_lds(q, cu, 0, 0, dp, dp)
+        assert np.array_equal(ok[0].view(np.uint16), q[:128, 0].view(np.uint16))
+        assert np.array_equal(got[0].view(np.uint16), ok[0].view(np.uint16))
+
+
+def test_q_block_staging_planted_unswizzled_copy():
+    """A copy that skips the K swizzle puts chunks where the reads do not look:
+    the model catches it."""
+    q = np.random.default_rng(1).standard_normal((256, 1, 128)).astype(np.float16)
+    cu = np.array([0, 256])
+    got, _ = q_block_through_lds(q, cu, 0, 0, 128, 128, copy_swizzle=False)
+    assert not np.array_equal(got[0].view(np.uint16), q[:128, 0].view(np.uint16))

@@ -132,6 +132,11 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
     set_error("%s: max_seqlen_k * token stride exceeds 2 GiB (%lld bytes)", fn, (long long)span);
     return TILEMIX_E_INVALID;
   }
+  // The 128-row Q block is copied through a raw buffer as well.
+  if ((int64_t)128 * p.stride_q_token * 2 >= ((int64_t)1 << 31)) {
+    set_error("%s: 128 * Q token stride exceeds 2 GiB", fn);
+    return TILEMIX_E_INVALID;
+  }
 
   const int m_blocks = (p.max_seqlen_q + wg_rows - 1) / wg_rows;
   const int64_t total = (int64_t)m_blocks * p.heads_q * p.batch;

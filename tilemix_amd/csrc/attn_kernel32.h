@@ -82,12 +82,17 @@ attn32_kernel(const AttnKArgs a) {
   constexpr int V8_INS = (64 * ROW8) / 1024 / NW;
   static_assert(K16_INS >= 1 && K8_INS >= 1 && V16_INS >= 1 && V8_INS >= 1, "tile split");
 
-  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE];
-  // Per-wave partial max of the in-kernel Q quantisation, in the last bytes of
-  // stage 1: that stage is first written after the loop's first barrier, when
-  // every wave has read these values.  (A separate array would push the split
-  // DP=128 workgroup past 80 KB and halve the workgroups per CU.)
-  float* const q_red = reinterpret_cast<float*>(smem + 2 * STAGE - 4 * NW);
+  // The Q block (128 rows) is staged through stage 1 in the prologue (that
+  // stage is first written by tile 1's copy, after the loop's first barrier).
+  // It fills a plain stage; a split stage has room after it.
+  constexpr int QBYTES = BM * ROW16;
+  static_assert(QBYTES <= STAGE, "Q block fits a stage");
+  constexpr int QRED_EXTRA = QBYTES + 4 * NW <= STAGE ? 0 : 4 * NW;
+  __shared__ __attribute__((aligned(1024))) unsigned char smem[2 * STAGE + QRED_EXTRA];
+  // Per-wave partial max of the in-kernel Q quantisation: after the Q block in
+  // stage 1 when it fits (split: a separate array would push the DP=128
+  // workgroup past 80 KB and halve the workgroups per CU), else after stage 1.
+  float* const q_red = reinterpret_cast<float*>(smem + (QRED_EXTRA ? 2 * STAGE : 2 * STAGE - 4 * NW));
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -372,6 +377,32 @@ attn32_kernel(const AttnKArgs a) {
     }
   };
 
+  // ---- Q block -> LDS stage 1 ----------------------------------------------
+  // The fp16 Q rows (QK operand and the in-kernel quantisation's input) are
+  // copied like a K tile: 1 KB per copy, 16 lanes per 256-byte row, the K
+  // swizzle, zeros past the sequence end (buffer size) and past head_dim
+  // (kOffOutside).  Wave w copies rows 32 w .. 32 w + 31 of the block, the rows
+  // it reads back, so it needs no barrier.  (Loading the fragments straight
+  // into registers touches 32 rows per load instruction.)  They go out before
+  // the first tile's copies, so the two latencies overlap.
+  const bool q_fused = MODE != TILEMIX_ROUTING_FP16 && a.q_fused;
+  const bool q_lds = MODE != TILEMIX_ROUTING_INT8 || q_fused;
+  if (q_lds) {
+    constexpr int QRPI = 1024 / ROW16, QCPR = ROW16 / 16, QINS = 32 / QRPI;
+    const int64_t qt_bytes = a.sq_t * 2;
+    const unsigned char* qwave =
+        reinterpret_cast<const unsigned char*>(a.q + (int64_t)(q_start + row0w) * a.sq_t + (int64_t)h * a.sq_h);
+    const SRsrc rs = make_srsrc(qwave, row0w < Lq ? (int)((Lq - row0w) * qt_bytes) : 0);
+    const uint32_t qlds = smem_lds + STAGE + (uint32_t)(wave * 32 * ROW16);
+#pragma unroll
+    for (int i = 0; i < QINS; ++i) {
+      const int rl = i * QRPI + lane / QCPR;  // row within the wave's 32
+      const int chunk = (lane % QCPR) ^ swz_k<ROW16>(wave * 32 + rl);
+      const int off = chunk * 16 >= 2 * a.d ? kOffOutside : (int)(rl * qt_bytes) + chunk * 16;
+      async_load16_asm(rs, off, qlds + (uint32_t)(i * QRPI * ROW16));
+    }
+  }
+
   // The first tile's copies go out before Q is loaded, so the two
   // latencies overlap.
   int route_next = 0;
@@ -389,16 +420,17 @@ attn32_kernel(const AttnKArgs a) {
   f16x8 qf[KS16];
   i32x4 q8f[KS8];
   f16 sq16 = (f16)1.0f;
-  const bool q_fused = MODE != TILEMIX_ROUTING_FP16 && a.q_fused;
   f16x8 qraw[KS16];
-  if (MODE != TILEMIX_ROUTING_INT8 || q_fused) {
-    const f16* qp = a.q + (int64_t)(q_start + row) * a.sq_t + (int64_t)h * a.sq_h;
+  if (q_lds) {
+    // The wave's own Q rows, copied above in the K-tile layout: row r, k-step
+    // s, half hi is logical chunk 2 s + hi of LDS row r (rows past the
+    // sequence end and columns past head_dim are zeros).  Its own copies
+    // only, so its own wait suffices.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    int qbase = (wave * 32 + l32) * ROW16 + ((16 * hi) ^ (16 * swz_k<ROW16>(l32)));
+    asm volatile("" : "+v"(qbase));
 #pragma unroll
-    for (int s = 0; s < KS16; ++s) {
-      const int d0 = 16 * s + 8 * hi;
-      qraw[s] = (f16x8){};
-      if (row_ok && d0 < a.d) qraw[s] = *reinterpret_cast<const f16x8*>(qp + d0);
-    }
+    for (int s = 0; s < KS16; ++s) qraw[s] = *reinterpret_cast<const f16x8*>(smem + STAGE + (qbase ^ (32 * s)));
   }
   if (MODE != TILEMIX_ROUTING_INT8) {
 #pragma unroll
