@@ -531,12 +531,16 @@ attn32_kernel(const AttnKArgs a) {
   const int half = SPLIT && wave >= NW / 2 ? 1 : 0;
   // Start of tile n, for every wave: the tile has landed (own loads), then
   // every wave's loads have landed and every wave is done with the other
-  // stage (tile n-1); then the next tile's copies go out.
-  auto tile_start = [&](int n) {
+  // stage (tile n-1), so the next tile's copies may go out from here on
+  // (tile_start issues them at once; the compute loop after the QK reads).
+  auto tile_wait = [&](int n) {
     const int route = SPLIT ? (route_next >> half) & 1 : route_next;
     __builtin_amdgcn_s_waitcnt(0);
     if (INT8V && route == 1) widen_v8(smem + (n & 1) * STAGE);
     __syncthreads();
+  };
+  auto tile_start = [&](int n) {
+    tile_wait(n);
     if (n + 1 < n_blocks)
       issue_next(n + 1, smem_lds + ((n + 1) & 1) * STAGE, route_next, sk_next, sv_next);
   };
@@ -776,10 +780,14 @@ attn32_kernel(const AttnKArgs a) {
       const f16 skc[NSG] = {sk_next[0]};
       const f16 svc[NSG] = {sv_next[0]};
       unsigned char* stage = smem + (n & 1) * STAGE;
-      tile_start(n);
+      tile_wait(n);
       const int key0 = n * kBN;
       uint32_t s16[2][8];
       tile_scores(stage, route, skc, key0, s16);
+      // The next tile's copies go out after this tile's K reads: the loop
+      // head's scalar work then no longer delays the QK chain.
+      if (n + 1 < n_blocks)
+        issue_next(n + 1, smem_lds + ((n + 1) & 1) * STAGE, route_next, sk_next, sv_next);
       tile_mask(key0, s16);
       const float mx = tile_max(s16);
       const bool has = mx != -INFINITY;
