@@ -2,10 +2,13 @@
 launch reads.
 
 The kernels copy every 64-key tile of K (fp16 or int8), V (fp16) and int8 V
-codes with ``buffer_load_dwordx4 ... lds`` through a raw buffer based at the
-tile's first key (sequence start + head offset) whose size is the bytes left
-to the sequence end; a 4-byte lane of the load reads memory only below that
-size (zeros otherwise).  The lane offsets restated here are those of
+codes with ``buffer_load_dwordx4 ... lds``.  The 32-row kernel reads through
+one raw buffer per stream based at the sequence's first key (sequence start +
+head offset) and sized to the sequence, adding the tile's byte offset to the
+32-bit lane offsets; the 16-row kernel's buffer is based at the tile's first
+key and sized to the bytes left to the sequence end.  A 4-byte lane of the load
+reads memory only below the buffer size (zeros otherwise).  The lane offsets
+restated here are those of
 ``lane_off0`` / ``issue_tile`` in tilemix_amd/csrc/attn_kernel32.h and of
 ``lane_off`` / ``issue_tile`` in tilemix_amd/csrc/attn_kernel16.h (swizzles:
 ``swz_k``, ``swz_v``, ``swz_v32`` in attn_common.h; out-of-range offset
@@ -71,16 +74,26 @@ def lane_offsets(kernel, rowb, tok_bytes, swz, valid_bytes, nw=4, mask=True):
     return np.array(offs, dtype=np.int64)
 
 
-def bytes_read(offs, lens, hk, tok_bytes, head_bytes):
+def tile_dwords(kernel, offs, L, t, tok_bytes):
+    """Byte offsets from the buffer base that the lanes of tile t read (dword
+    starts), and the buffer size: the 32-row kernel's buffer spans the sequence
+    and the tile offset is added in 32 bits; the 16-row kernel's starts at the
+    tile."""
+    dw = offs[:, None] + 4 * np.arange(4)[None, :]  # every dword of every lane
+    if kernel == 32:
+        return (dw + 64 * t * tok_bytes) & 0xFFFFFFFF, L * tok_bytes
+    return dw, (L - 64 * t) * tok_bytes
+
+
+def bytes_read(offs, lens, hk, tok_bytes, head_bytes, kernel=32):
     """Relative byte addresses (from the tensor's data pointer) read by the copies."""
     out = []
     cu = np.concatenate([[0], np.cumsum(lens)])
-    dw = offs[:, None] + 4 * np.arange(4)[None, :]  # every dword of every lane
     for z, L in enumerate(lens):
         for h in range(hk):
             for t in range((L + 63) // 64):
-                base = (cu[z] + 64 * t) * tok_bytes + h * head_bytes
-                size = (L - 64 * t) * tok_bytes
+                dw, size = tile_dwords(kernel, offs, L, t, tok_bytes)
+                base = (cu[z] + (64 * t if kernel != 32 else 0)) * tok_bytes + h * head_bytes
                 hit = dw[dw < size]
                 out.append((base + hit[:, None] + np.arange(4)[None, :]).ravel())
     return np.concatenate(out) if out else np.zeros(0, dtype=np.int64)
@@ -131,7 +144,7 @@ def _streams(kernel, dp, d, hstride, hk):
 def test_copies_read_only_valid_elements(kernel, d, dp, hk, hstride, lens):
     for name, rowb, tok, head, elem, valid, swz in _streams(kernel, dp, d, hstride, hk):
         offs = lane_offsets(kernel, rowb, tok, swz, valid)
-        addr = bytes_read(offs, lens, hk, tok, head)
+        addr = bytes_read(offs, lens, hk, tok, head, kernel)
         assert addr.size > 0
         bad = check_elements(addr, lens, hk, tok, head, elem, d)
         assert bad == 0, f"{name}: {bad} bytes outside the valid elements"
@@ -144,10 +157,45 @@ def test_planted_unmasked_copy_reads_past_the_end(kernel):
     d, dp, hk, lens = 80, 128, 3, [1, 63, 64, 65, 130]
     name, rowb, tok, head, elem, valid, swz = _streams(kernel, dp, d, d, hk)[0]
     offs = lane_offsets(kernel, rowb, tok, swz, valid, mask=False)
-    addr = bytes_read(offs, lens, hk, tok, head)
+    addr = bytes_read(offs, lens, hk, tok, head, kernel)
     n_bytes = sum(lens) * tok
     assert addr.max() >= n_bytes  # past the end of the allocation
     assert check_elements(addr, lens, hk, tok, head, elem, d) > 0
+
+
+def _outside_lanes_in_range(L, tok, d=80, dp=128):
+    """Dwords of padded-column lanes (kOffOutside) of the 32-row kernel's K
+    copies that land inside the sequence's buffer, over all tiles of a
+    sequence of L keys (the tile offset added in 32 bits)."""
+    rowb = 2 * dp
+    offs = lane_offsets(32, rowb, tok, swz_k, 2 * d)
+    outside = offs[offs >= OUTSIDE]
+    assert outside.size > 0
+    n_in = 0
+    for t in range((L + 63) // 64):
+        dw, size = tile_dwords(32, outside, L, t, tok)
+        n_in += int((dw < size).sum())
+    return n_in
+
+
+def test_span_check_keeps_padded_lanes_out_of_range():
+    """attn.hip rejects (max_seqlen_k + 64) * token stride >= 2^31: at the
+    largest accepted length, no padded-column lane's offset (0x80000000 + tile
+    offset + copy step) wraps past 2^32 back into the buffer."""
+    tok = 3 << 18  # 768 KiB per token: a few thousand keys reach the limit
+    L = ((1 << 31) - 1) // tok - 64
+    assert (L + 64) * tok < 1 << 31
+    assert _outside_lanes_in_range(L, tok) == 0
+
+
+def test_planted_span_check_without_slack_wraps():
+    """With the check as max(max_seqlen_k, 64) * token stride < 2^31 (no
+    64-row slack), the longest accepted sequence lets padded-column offsets
+    of its last tiles wrap into the buffer: the slack is needed."""
+    tok = 3 << 18
+    L = ((1 << 31) - 1) // tok
+    assert max(L, 64) * tok < 1 << 31
+    assert _outside_lanes_in_range(L, tok) > 0
 
 
 def test_lds_receives_every_valid_chunk_once():

@@ -124,12 +124,12 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   }
 
   // K/V tiles are read through 32-bit raw buffers spanning one sequence; the
-  // per-lane offsets of a tile reach 64 rows even when the sequence is shorter.
-  const int64_t span = (int64_t)std::max(p.max_seqlen_k, 64) *
+  // per-lane offsets of the last tile reach up to 64 rows past its end.
+  const int64_t span = ((int64_t)p.max_seqlen_k + 64) *
                        (int64_t)std::max(std::max(p.stride_k_token, p.stride_v_token) * 2,
                                          std::max(p.stride_k8_token, p.stride_v8_token));
   if (span >= ((int64_t)1 << 31)) {
-    set_error("%s: max_seqlen_k * token stride exceeds 2 GiB (%lld bytes)", fn, (long long)span);
+    set_error("%s: (max_seqlen_k + 64) * token stride exceeds 2 GiB (%lld bytes)", fn, (long long)span);
     return TILEMIX_E_INVALID;
   }
   // The 128-row Q block is copied through a raw buffer as well.

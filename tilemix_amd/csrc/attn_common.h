@@ -179,9 +179,10 @@ struct SRsrc {
   i32x4 w;
 };
 // A lane offset past every buffer's size: the copy reads nothing and writes
-// zeros.  The host checks 64 * token stride < 2^31 bytes, so the buffers span
-// less than 2^31 bytes and the row offsets of a tile (< 64 rows) added to this
-// value stay below 2^32 (no wrap back into range).
+// zeros.  The host checks (max_seqlen_k + 64) * token stride < 2^31 bytes, so
+// a sequence's buffer spans less than 2^31 bytes and a tile's offset plus the
+// row offsets of its 64 rows, added to this value, stay below 2^32 (no wrap
+// back into range).
 constexpr int kOffOutside = (int)0x80000000u;
 __device__ __forceinline__ SRsrc make_srsrc(const void* base, int bytes) {
   const uint64_t p = reinterpret_cast<uint64_t>(base);

@@ -146,10 +146,10 @@ attn32_kernel(const AttnKArgs a) {
   const bool row_ok = row < Lq;
 
   // ---- asynchronous tile loads (HBM -> LDS, no registers) -----------------
-  // Each tile is fetched through raw buffers based at the tile's first key
-  // and sized to the keys left in the sequence: rows past the end read as 0
-  // (finite bytes for masked keys, which contribute exactly 0 through p = 0).
-  // Per-lane offsets are loop-invariant; the per-tile work is scalar.  The
+  // Each stream is one raw buffer over the sequence's keys (built once per
+  // item); a tile adds its byte offset to the lane offsets, and rows past the
+  // end read as 0 (finite bytes for masked keys, which contribute exactly 0
+  // through p = 0).  Per-lane offsets are loop-invariant.  The
   // swizzle of a copied row depends only on its index mod 16, and the rows of
   // copy i are those of copy 0 plus i * NW * rows-per-copy (a multiple of 16),
   // so one lane offset per stream serves every copy of a tile.
@@ -187,33 +187,35 @@ attn32_kernel(const AttnKArgs a) {
   const int step_v8 = NW * (1024 / ROW8) * (int)v8t_bytes;
   const uint32_t smem_lds = lds_addr(smem);
   // route: 0 fp16 / 1 int8; SPLIT: bit 0 the low half's route, bit 1 the high half's.
-  // Base of the next tile in each stream and the bytes from there to the end
-  // of the sequence, advanced by one tile per issue (tiles are issued in
-  // order, one per call): no 64-bit multiplies in the loop.
-  const unsigned char* kcur = kseq;
-  const unsigned char* k8cur = k8seq;
-  const unsigned char* vcur = vseq;
-  const unsigned char* v8cur = v8seq;
-  int kleft = (int)(Lk * kt_bytes), k8left = (int)(Lk * k8t_bytes);
-  int vleft = (int)(Lk * vt_bytes), v8left = (int)(Lk * v8t_bytes);
+  // Byte offset of the next tile in each stream, advanced by one tile per
+  // issue (tiles are issued in order, one per call; GEN steps set it from the
+  // tile index): one scalar add per stream and tile, the buffer descriptors
+  // stay fixed.
+  const SRsrc rs_k16 = make_srsrc(kseq, (int)(Lk * kt_bytes));
+  const SRsrc rs_k8 = make_srsrc(k8seq, (int)(Lk * k8t_bytes));
+  const SRsrc rs_v16 = make_srsrc(vseq, (int)(Lk * vt_bytes));
+  const SRsrc rs_v8 = make_srsrc(v8seq, (int)(Lk * v8t_bytes));
+  int toff_k16 = 0, toff_k8 = 0, toff_v16 = 0, toff_v8 = 0;
+  const int tstep_k16 = kBN * (int)kt_bytes, tstep_k8 = kBN * (int)k8t_bytes;
+  const int tstep_v16 = kBN * (int)vt_bytes, tstep_v8 = kBN * (int)v8t_bytes;
   // with_v = false (a GEN max pass) copies the K tile only.
   auto issue_tile = [&](int route, uint32_t stage, bool with_v) {
     const bool need16 = MODE != TILEMIX_ROUTING_INT8 && (SPLIT ? route != 3 : route == 0);
     const bool need8 = MODE != TILEMIX_ROUTING_FP16 && route != 0;
     if (need16) {
-      const SRsrc rs = make_srsrc(kcur, kleft);
+      const SRsrc rs = rs_k16;
       // Opaque copy of the lane offset: the per-copy sums are formed here, one
       // add each, instead of being hoisted into loop-invariant VGPRs (the
       // same for the LDS read bases below).
-      int o = dma_k16;
+      int o = dma_k16 + toff_k16;
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < K16_INS; ++i)
         async_load16_asm(rs, o + i * step_k16, stage + (i * NW + wave) * 1024);
     }
     if (need8) {
-      const SRsrc rs = make_srsrc(k8cur, k8left);
-      int o = dma_k8;
+      const SRsrc rs = rs_k8;
+      int o = dma_k8 + toff_k8;
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < K8_INS; ++i)
@@ -222,32 +224,24 @@ attn32_kernel(const AttnKArgs a) {
     const uint32_t vstage = stage + KBUF;
     if (!with_v) {
     } else if (!INT8V || route == 0) {
-      const SRsrc rs = make_srsrc(vcur, vleft);
-      int o = dma_v16;
+      const SRsrc rs = rs_v16;
+      int o = dma_v16 + toff_v16;
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < V16_INS; ++i)
         async_load16_asm(rs, o + i * step_v16, vstage + (i * NW + wave) * 1024);
     } else {
-      const SRsrc rs = make_srsrc(v8cur, v8left);
-      int o = dma_v8;
+      const SRsrc rs = rs_v8;
+      int o = dma_v8 + toff_v8;
       asm volatile("" : "+v"(o));
 #pragma unroll
       for (int i = 0; i < V8_INS; ++i)
         async_load16_asm(rs, o + i * step_v8, stage + V8OFF + (i * NW + wave) * 1024);
     }
-    kcur += kBN * kt_bytes;
-    kleft -= kBN * (int)kt_bytes;
-    vcur += kBN * vt_bytes;
-    vleft -= kBN * (int)vt_bytes;
-    if (MODE != TILEMIX_ROUTING_FP16) {
-      k8cur += kBN * k8t_bytes;
-      k8left -= kBN * (int)k8t_bytes;
-    }
-    if (INT8V) {
-      v8cur += kBN * v8t_bytes;
-      v8left -= kBN * (int)v8t_bytes;
-    }
+    toff_k16 += tstep_k16;
+    toff_v16 += tstep_v16;
+    if (MODE != TILEMIX_ROUTING_FP16) toff_k8 += tstep_k8;
+    if (INT8V) toff_v8 += tstep_v8;
   };
 
   // int8 V codes -> fp16 V tile (the layout of an fp16 V copy).  Each wave
@@ -357,19 +351,10 @@ attn32_kernel(const AttnKArgs a) {
   // steps revisit tiles), and a max pass copies K only.
   auto issue_step = [&](const Step& s, uint32_t stage, int& route, f16 (&skv)[NSG], f16 (&svv)[NSG]) {
     route = tile_route(s.n, s.n / a.mask_tiles);
-    const int key0 = s.n * kBN;
-    kcur = kseq + (int64_t)key0 * kt_bytes;
-    kleft = (int)((Lk - key0) * kt_bytes);
-    vcur = vseq + (int64_t)key0 * vt_bytes;
-    vleft = (int)((Lk - key0) * vt_bytes);
-    if (MODE != TILEMIX_ROUTING_FP16) {
-      k8cur = k8seq + (int64_t)key0 * k8t_bytes;
-      k8left = (int)((Lk - key0) * k8t_bytes);
-    }
-    if (INT8V) {
-      v8cur = v8seq + (int64_t)key0 * v8t_bytes;
-      v8left = (int)((Lk - key0) * v8t_bytes);
-    }
+    toff_k16 = s.n * tstep_k16;
+    toff_v16 = s.n * tstep_v16;
+    if (MODE != TILEMIX_ROUTING_FP16) toff_k8 = s.n * tstep_k8;
+    if (INT8V) toff_v8 = s.n * tstep_v8;
     issue_tile(route, stage, s.pass == 1);
     if (MODE != TILEMIX_ROUTING_FP16 && route != 0) {
       group_scales(s.n, a.sk + hk, ks_base, ks_end, has_ks, skv);
