@@ -112,7 +112,9 @@ int tilemix_quant_per_block_int8(const tilemix_quant_params* p, void* stream);
  * Supported by this build: block_m in {64, 128}; block_n in {64, 128, 256};
  * block_n_mask a multiple of block_n with ceil(max_seqlen_k/block_n_mask) <= 64;
  * head_dim a multiple of 16, <= 128 (the Python layer zero-pads other widths);
- * blkk a positive multiple of 4; fp16 data.  block_n = 64 with blkk a multiple
+ * blkk a positive multiple of 4; fp16 data; (max_seqlen_k + 64) times the
+ * largest K/V token stride in bytes below 2 GiB and 128 Q token strides below
+ * 2 GiB (tiles are read through 32-bit buffer offsets).  block_n = 64 with blkk a multiple
  * of 64 runs the fastest kernels; other shapes run variants that stream each
  * block_n tile twice (max pass, then update pass) and look scales up per key.
  */
