@@ -388,8 +388,8 @@ attn32_kernel(const AttnKArgs a) {
     }
   }
 
-  // The first tile's copies go out before Q is loaded, so the two
-  // latencies overlap.
+  // The first tile's copies go out right behind the Q copies, before Q is
+  // read back, so the two latencies overlap.
   int route_next = 0;
   f16 sk_next[NSG], sv_next[NSG];
 #pragma unroll
