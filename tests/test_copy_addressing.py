@@ -2,13 +2,11 @@
 launch reads.
 
 The kernels copy every 64-key tile of K (fp16 or int8), V (fp16) and int8 V
-codes with ``buffer_load_dwordx4 ... lds``.  The 32-row kernel reads through
-one raw buffer per stream based at the sequence's first key (sequence start +
-head offset) and sized to the sequence, adding the tile's byte offset to the
-32-bit lane offsets; the 16-row kernel's buffer is based at the tile's first
-key and sized to the bytes left to the sequence end.  A 4-byte lane of the load
-reads memory only below the buffer size (zeros otherwise).  The lane offsets
-restated here are those of
+codes with ``buffer_load_dwordx4 ... lds``.  Both kernels read through one raw
+buffer per stream based at the sequence's first key (sequence start + head
+offset) and sized to the sequence, adding the tile's byte offset to the 32-bit
+lane offsets.  A 4-byte lane of the load reads memory only below the buffer
+size (zeros otherwise).  The lane offsets restated here are those of
 ``lane_off0`` / ``issue_tile`` in tilemix_amd/csrc/attn_kernel32.h and of
 ``lane_off`` / ``issue_tile`` in tilemix_amd/csrc/attn_kernel16.h (swizzles:
 ``swz_k``, ``swz_v``, ``swz_v32`` in attn_common.h; out-of-range offset
@@ -76,13 +74,10 @@ def lane_offsets(kernel, rowb, tok_bytes, swz, valid_bytes, nw=4, mask=True):
 
 def tile_dwords(kernel, offs, L, t, tok_bytes):
     """Byte offsets from the buffer base that the lanes of tile t read (dword
-    starts), and the buffer size: the 32-row kernel's buffer spans the sequence
-    and the tile offset is added in 32 bits; the 16-row kernel's starts at the
-    tile."""
+    starts), and the buffer size: the buffer spans the sequence and the tile
+    offset is added in 32 bits (both kernels)."""
     dw = offs[:, None] + 4 * np.arange(4)[None, :]  # every dword of every lane
-    if kernel == 32:
-        return (dw + 64 * t * tok_bytes) & 0xFFFFFFFF, L * tok_bytes
-    return dw, (L - 64 * t) * tok_bytes
+    return (dw + 64 * t * tok_bytes) & 0xFFFFFFFF, L * tok_bytes
 
 
 def bytes_read(offs, lens, hk, tok_bytes, head_bytes, kernel=32):
@@ -93,7 +88,7 @@ def bytes_read(offs, lens, hk, tok_bytes, head_bytes, kernel=32):
         for h in range(hk):
             for t in range((L + 63) // 64):
                 dw, size = tile_dwords(kernel, offs, L, t, tok_bytes)
-                base = (cu[z] + (64 * t if kernel != 32 else 0)) * tok_bytes + h * head_bytes
+                base = cu[z] * tok_bytes + h * head_bytes
                 hit = dw[dw < size]
                 out.append((base + hit[:, None] + np.arange(4)[None, :]).ravel())
     return np.concatenate(out) if out else np.zeros(0, dtype=np.int64)
@@ -163,29 +158,30 @@ def test_planted_unmasked_copy_reads_past_the_end(kernel):
     assert check_elements(addr, lens, hk, tok, head, elem, d) > 0
 
 
-def _outside_lanes_in_range(L, tok, d=80, dp=128):
-    """Dwords of padded-column lanes (kOffOutside) of the 32-row kernel's K
-    copies that land inside the sequence's buffer, over all tiles of a
-    sequence of L keys (the tile offset added in 32 bits)."""
+def _outside_lanes_in_range(kernel, L, tok, d=80, dp=128):
+    """Dwords of padded-column lanes (kOffOutside) of a kernel's K copies that
+    land inside the sequence's buffer, over all tiles of a sequence of L keys
+    (the tile offset added in 32 bits)."""
     rowb = 2 * dp
-    offs = lane_offsets(32, rowb, tok, swz_k, 2 * d)
+    offs = lane_offsets(kernel, rowb, tok, swz_k, 2 * d)
     outside = offs[offs >= OUTSIDE]
     assert outside.size > 0
     n_in = 0
     for t in range((L + 63) // 64):
-        dw, size = tile_dwords(32, outside, L, t, tok)
+        dw, size = tile_dwords(kernel, outside, L, t, tok)
         n_in += int((dw < size).sum())
     return n_in
 
 
-def test_span_check_keeps_padded_lanes_out_of_range():
+@pytest.mark.parametrize("kernel", [32, 16])
+def test_span_check_keeps_padded_lanes_out_of_range(kernel):
     """attn.hip rejects (max_seqlen_k + 64) * token stride >= 2^31: at the
     largest accepted length, no padded-column lane's offset (0x80000000 + tile
     offset + copy step) wraps past 2^32 back into the buffer."""
     tok = 3 << 18  # 768 KiB per token: a few thousand keys reach the limit
     L = ((1 << 31) - 1) // tok - 64
     assert (L + 64) * tok < 1 << 31
-    assert _outside_lanes_in_range(L, tok) == 0
+    assert _outside_lanes_in_range(kernel, L, tok) == 0
 
 
 def test_planted_span_check_without_slack_wraps():
@@ -195,7 +191,7 @@ def test_planted_span_check_without_slack_wraps():
     tok = 3 << 18
     L = ((1 << 31) - 1) // tok
     assert max(L, 64) * tok < 1 << 31
-    assert _outside_lanes_in_range(L, tok) > 0
+    assert _outside_lanes_in_range(32, L, tok) > 0
 
 
 def test_lds_receives_every_valid_chunk_once():

@@ -171,9 +171,12 @@ attn16_kernel(const AttnKArgs a) {
   };
 
   // ---- asynchronous tile loads (HBM -> LDS, no registers) -----------------
-  // Each tile is fetched through raw buffers based at the tile's first key
-  // and sized to the keys left in the sequence: rows past the end read as 0
-  // (finite bytes for masked keys, which contribute exactly 0 through p = 0).
+  // Each stream is one raw buffer over the sequence's keys (built once per
+  // item); a tile adds its byte offset to the lane offsets, and rows past the
+  // end read as 0 (finite bytes for masked keys, which contribute exactly 0
+  // through p = 0).  The host keeps (max_seqlen_k + 64) * token stride below
+  // 2^31 bytes, so the sums stay below 2^31 and a padded-column lane's offset
+  // (kOffOutside + tile offset) below 2^32.
   const int64_t kt_bytes = a.sk_t * 2, vt_bytes = a.sv_t * 2;
   const int64_t k8t_bytes = a.sk8_t, v8t_bytes = a.sv8_t;
   const unsigned char* kseq = reinterpret_cast<const unsigned char*>(a.k + (int64_t)k_start * a.sk_t + (int64_t)hk * a.sk_h);
@@ -199,40 +202,43 @@ attn16_kernel(const AttnKArgs a) {
   // Copies are issued from inline assembly (async_load16_asm): the loop
   // orders them against its LDS reads itself (s_waitcnt + barrier per tile).
   const uint32_t smem_lds = lds_addr(smem);
+  const SRsrc rs_k16 = make_srsrc(kseq, (int)(Lk * kt_bytes));
+  const SRsrc rs_k8 = make_srsrc(k8seq, (int)(Lk * k8t_bytes));
+  const SRsrc rs_v16 = make_srsrc(vseq, (int)(Lk * vt_bytes));
+  const SRsrc rs_v8 = make_srsrc(v8seq, (int)(Lk * v8t_bytes));
   // with_v = false (a GEN max pass) copies the K tile only.
   auto issue_tile = [&](int n, int route, uint32_t stage, bool with_v) {
     const int key0 = n * kBN;
-    const int rem = Lk - key0;  // >= 1
     if (route == 0) {
-      const SRsrc rs = make_srsrc(kseq + key0 * kt_bytes, (int)(rem * kt_bytes));
+      const int toff = key0 * (int)kt_bytes;
 #pragma unroll
       for (int i = 0; i < K16_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K16_T) async_load16_asm(rs, lane_off(L, ROW16, kt_bytes, 0), stage + L * 1024);
+        if (L < K16_T) async_load16_asm(rs_k16, lane_off(L, ROW16, kt_bytes, 0) + toff, stage + L * 1024);
       }
     } else {
-      const SRsrc rs = make_srsrc(k8seq + key0 * k8t_bytes, (int)(rem * k8t_bytes));
+      const int toff = key0 * (int)k8t_bytes;
 #pragma unroll
       for (int i = 0; i < K8_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K8_T) async_load16_asm(rs, lane_off(L, ROW8, k8t_bytes, 0), stage + L * 1024);
+        if (L < K8_T) async_load16_asm(rs_k8, lane_off(L, ROW8, k8t_bytes, 0) + toff, stage + L * 1024);
       }
     }
     const uint32_t vstage = stage + KBUF;
     if (!with_v) {
     } else if (!INT8V || route == 0) {
-      const SRsrc rs = make_srsrc(vseq + key0 * vt_bytes, (int)(rem * vt_bytes));
+      const int toff = key0 * (int)vt_bytes;
 #pragma unroll
       for (int i = 0; i < K16_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K16_T) async_load16_asm(rs, lane_off(L, ROW16, vt_bytes, 1), vstage + L * 1024);
+        if (L < K16_T) async_load16_asm(rs_v16, lane_off(L, ROW16, vt_bytes, 1) + toff, vstage + L * 1024);
       }
     } else {
-      const SRsrc rs = make_srsrc(v8seq + key0 * v8t_bytes, (int)(rem * v8t_bytes));
+      const int toff = key0 * (int)v8t_bytes;
 #pragma unroll
       for (int i = 0; i < K8_I; ++i) {
         const int L = i * NW + wave;
-        if (L < K8_T) async_load16_asm(rs, lane_off(L, ROW8, v8t_bytes, 0), stage + V8OFF + L * 1024);
+        if (L < K8_T) async_load16_asm(rs_v8, lane_off(L, ROW8, v8t_bytes, 0) + toff, stage + V8OFF + L * 1024);
       }
     }
   };
