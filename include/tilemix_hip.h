@@ -101,20 +101,23 @@ int tilemix_quant_per_block_int8(const tilemix_quant_params* p, void* stream);
  * (hk = h / (heads_q/heads_k)).  The K (and V) scale of key n is
  * sk[cu_k_scale[z] + n / blkk], clamped to the sequence's last scale row.
  *
- * q_quant_in_kernel = 1 (blkq == 128, routing not FP16, and block_m == 128 or
- * block_m == 64 unless mixed routing runs on int8 V codes): each 128-row
+ * q_quant_in_kernel = 1 (blkq == 128, routing not FP16, and block_m 128, 256 or
+ * 512, or block_m 64 unless mixed routing runs on int8 V codes): each 128-row
  * workgroup quantises its own 128-row Q block (scale = max|q|/127, code =
  * trunc(q/scale +- 0.5), exactly quant_per_block_int8 with sm_scale = 1, the
  * way tilemix_attention_with_quant quantises Q, tilemix.py:126-140) instead of
  * reading q8/sq/cu_q_scale, which may then be NULL.  This removes the Q
  * pre-pass of tilemix_attention_with_quant; the reference has no such field.
  *
- * Supported by this build: block_m in {64, 128}; block_n in {64, 128, 256};
+ * Supported by this build: block_m in {64, 128, 256, 512}; block_n in {64, 128, 256};
  * block_n_mask a multiple of block_n with ceil(max_seqlen_k/block_n_mask) <= 64;
  * head_dim a multiple of 16, <= 128 (the Python layer zero-pads other widths);
  * blkk a positive multiple of 4; fp16 data; (max_seqlen_k + 64) times the
  * largest K/V token stride in bytes below 2 GiB and 128 Q token strides below
- * 2 GiB (tiles are read through 32-bit buffer offsets).  block_n = 64 with blkk a multiple
+ * 2 GiB (tiles are read through 32-bit buffer offsets; the Python layer passes
+ * a head-major copy of a stream whose strides exceed it, as the reference
+ * addresses any strides with 64-bit pointers, tilemix.py:1259-1275).
+ * block_n = 64 with blkk a multiple
  * of 64 runs the fastest kernels; other shapes run variants that stream each
  * block_n tile twice (max pass, then update pass) and look scales up per key.
  */

@@ -47,6 +47,12 @@ Parity pinning of each function (see tests/test_oracle.py):
   against an fp64 softmax(QK^T)V within fp16 rounding; a planted-mistake set
   (dropped 1/l, wrong causal offset, wrong GQA mapping, wrong route bit) must
   fail; INT8 route checked against the dequantised fp64 computation.
+* int8 V codes (int8_use_fp16_v=False): fp64 attention over dequantised
+  scores and dequantised V (BLKK 64 and 16) and a known answer in which the
+  fp16 rounding of p * sv decides the output.
+* bias: a known answer in which LOG2E taken at fp16 decides a score, fp64
+  attention over scores + bias, and the batch-0 bias read in a two-sequence
+  launch.
 """
 from __future__ import annotations
 

@@ -210,6 +210,46 @@ def test_lds_receives_every_valid_chunk_once():
 
 
 # ---------------------------------------------------------------- Q block copy
+def q_copy_size(lq, row0w, tok, wave_rows=True):
+    """Byte size of a wave's Q buffer as the kernel stores it: a 32-bit value
+    (make_srsrc takes an int), sized to the rows the wave reads (at most 32);
+    ``wave_rows=False`` plants the size of every row left in the sequence."""
+    if row0w >= lq:
+        return 0
+    rows = min(lq - row0w, 32) if wave_rows else lq - row0w
+    return (rows * tok) & 0xFFFFFFFF
+
+
+def q_padded_lanes_inside(lq, tok, d=80, dp=128, wave_rows=True):
+    """Dwords of the Q copies' padded-column lanes (kOffOutside) that land
+    inside their wave's buffer, over every wave of every query block of a
+    sequence of lq rows with token stride tok bytes.  (The swizzle depends on
+    the row mod 16, so every wave has the same padded lanes.)"""
+    row16 = 2 * dp
+    qrpi, qcpr = 1024 // row16, row16 // 16
+    offs = []
+    for i in range(32 // qrpi):
+        for lane in range(64):
+            rl = i * qrpi + lane // qcpr
+            if ((lane % qcpr) ^ swz_k(row16, rl)) * 16 >= 2 * d:
+                offs += [OUTSIDE + 4 * dw for dw in range(4)]
+    offs = np.array(offs, dtype=np.int64)
+    sizes = np.array([q_copy_size(lq, r, tok, wave_rows) for r in range(0, lq, 32)], dtype=np.int64)
+    return int((offs[None, :] < sizes[:, None]).sum())
+
+
+def test_q_buffer_size_is_the_waves_rows():
+    """d = 80 with 32 query heads (5120-byte tokens) and 2^20 query rows: the
+    sequence's remaining rows span more than 2^31 bytes, but a wave's buffer is
+    sized to its 32 rows, so no padded-column lane reads inside it.  Sized to
+    the rest of the sequence (planted), the 32-bit size lets those lanes read
+    2 GiB past the wave's rows."""
+    lq, tok = 1 << 20, 2 * 80 * 32
+    assert 128 * tok < 1 << 31  # the host's Q stride check passes
+    assert q_padded_lanes_inside(lq, tok) == 0
+    assert q_padded_lanes_inside(lq, tok, wave_rows=False) > 0
+
+
 def q_block_through_lds(q, cu, h, m, d, dp, read_swz_from_block_row=False, copy_swizzle=True):
     """Model of the 32-row kernel's Q staging for query block m (128 rows) of
     every sequence, head h: each wave w copies rows 32 w .. 32 w + 31 of the
@@ -233,7 +273,7 @@ def q_block_through_lds(q, cu, h, m, d, dp, read_swz_from_block_row=False, copy_
         for w in range(4):
             row0w = m * 128 + 32 * w
             base = (int(cu[z]) + row0w) * tok + h * 2 * hstride
-            size = (lq - row0w) * tok if row0w < lq else 0
+            size = q_copy_size(lq, row0w, tok)
             for i in range(qins):
                 for lane in range(64):
                     rl = i * qrpi + lane // qcpr

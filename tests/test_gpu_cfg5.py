@@ -6,11 +6,17 @@ hidden 3072, 24/8 heads, head_dim 128, SwiGLU 8192, vocab 128256, RoPE theta
   reference harness, examples/benchmark_prefill.py:41-78): finite logits,
   every layer's cache holds the 4096 tokens, and the prefill-helper path gives
   the plain path's last-position top-1 with close logits.
+* Teacher-forced parity of every layer on the real B8 x 4096 activations: the
+  q/k/v each of the 28 TileMix calls receives (post-RoPE, not N(0,1) data) are
+  captured with the kernel's output, and three query blocks per layer (first,
+  middle, last) are recomputed by the CPU oracle on exactly that sub-problem.
+  This isolates the kernel from the growth of ulp-level differences through
+  28 layers.
 * Agreement with the same 28-layer model whose attention calls are answered by
   the CPU oracle (everything else identical, on the GPU), at a length the
-  oracle can afford: top-1 of the logits at every position of 8 sequences x 256
-  tokens (2048 positions, the last of each sequence among them), beside the
-  same comparison between two variants of the oracle (see the test).
+  oracle can afford: top-1 of the logits at every position of 12 sequences x
+  256 tokens (3072 positions, the last of each sequence among them), on the
+  positions where two valid oracle models agree, beside the all-position rate.
 """
 from __future__ import annotations
 
@@ -19,6 +25,7 @@ import pytest
 import torch
 from transformers import LlamaConfig, LlamaForCausalLM
 
+from oracle import tilemix_oracle as O
 from tests.test_gpu_models import _oracle_varlen_attention
 from tilemix_amd.models import tilemix_llama as TL
 
@@ -69,6 +76,91 @@ def test_cfg5_prefill_b8x4096(device, cfg5_model):
     assert diff.max().item() < 5e-2
 
 
+# (sequence, 128-row query block) pairs checked in every layer: first, middle, last.
+CFG5_BLOCKS = ((0, 0), (3, 15), (7, 31))
+
+
+def _oracle_sub_block(q, k, v, pmap, z, m, block_m, block_n, bnm, scale, accum):
+    """Oracle output of rows [m bm, m bm + bm) of sequence z of one dense-entry
+    call (q [Hq, rows, D], k/v [Hk, keys, D] already cut to the block's rows and
+    to the keys up to its last row): with causal attention those rows depend on
+    nothing else, and the Q / K quantisation blocks are the full call's (BLKQ
+    128 over the block's rows, BLKK 64 from the sequence's first key)."""
+    hq, rows, d = q.shape
+    hk, kend, _ = k.shape
+    qs = np.ascontiguousarray(q.transpose(1, 0, 2))
+    ks = np.ascontiguousarray(k.transpose(1, 0, 2))
+    vs = np.ascontiguousarray(v.transpose(1, 0, 2))
+    cuq, cuk = np.array([0, rows]), np.array([0, kend])
+    mbz = pmap.size // hk
+    sub_bits = np.array([int(pmap[h * mbz + m]) for h in range(hk)], dtype=np.uint64)
+    q8, sq, cuqs = O.quant_per_block_int8(qs, cuq, 128)
+    k8, sk, cuks = O.quant_per_block_int8(ks, cuk, 64)
+    out = O.attn_fwd(qs, ks, vs, cuq, cuk, sub_bits, block_m=block_m, block_n_mask=bnm, causal=True,
+                     sm_scale=scale, q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
+                     cu_q_scale=cuqs, cu_k_scale=cuks, fp16_accum=accum, block_n=block_n)
+    return out.transpose(1, 0, 2)
+
+
+@pytest.mark.timeout(900)
+def test_cfg5_per_layer_attention_parity(device, cfg5_model, monkeypatch):
+    """Every one of the 28 TileMix attention calls of the B8 x 4096 SpTrans50
+    prefill, on its real inputs: the kernel's rows of three query blocks per
+    layer against the oracle on the same sub-problem.  Bar per layer and block:
+    max-abs 2e-3 / mean-abs 2e-4 against the oracle with fp32 accumulation per
+    16-wide k-step (the MFMA's order), and mean-abs 2e-4 with 99.9% of elements
+    within 2e-3 against the exact-sum oracle (the definition; one fp16 ulp of
+    an FP16-route score can move a peaked row by more than 2e-3, see
+    tests/test_accumulation_models.py)."""
+    model = cfg5_model
+    vocab = model.config.vocab_size
+    ids = torch.randint(100, vocab, (8, 4096), generator=torch.Generator().manual_seed(0)).to(device)
+    captured = []
+    real = TL.tilemix_varlen_attention
+
+    def spy(q, k, v, block_m, block_n, **kw):
+        out = real(q, k, v, block_m, block_n, **kw)
+        blocks = []
+        for z, m in CFG5_BLOCKS:
+            r0, r1 = m * 128, min((m + 1) * 128, q.shape[2])
+            blocks.append((z, m, q[z, :, r0:r1].cpu().numpy(), k[z, :, :r1].cpu().numpy(),
+                           v[z, :, :r1].cpu().numpy(), out[z, :, r0:r1].cpu().numpy()))
+        captured.append(dict(block_m=block_m, block_n=block_n, bnm=kw.get("block_n_mask") or block_n,
+                             scale=kw["scale"], causal=kw["causal"], blocks=blocks,
+                             pmap=np.array([int(x) for x in kw["precision_map_all"].reshape(-1).tolist()],
+                                           dtype=np.uint64)))
+        return out
+
+    monkeypatch.setattr(TL, "tilemix_varlen_attention", spy)
+    with torch.no_grad():
+        model(ids, use_cache=False, logits_to_keep=1)
+    torch.cuda.synchronize()
+    monkeypatch.undo()
+    assert len(captured) == model.config.num_hidden_layers
+    worst = {"k16_max": 0.0, "k16_mean": 0.0, "exact_max": 0.0, "exact_mean": 0.0, "exact_within": 1.0}
+    for layer, c in enumerate(captured):
+        assert c["causal"] and c["block_m"] == 128, (c["block_m"], c["causal"])
+        line = []
+        for z, m, qb, kb, vb, ob in c["blocks"]:
+            got = ob.astype(np.float64)
+            assert np.isfinite(got).all()
+            args = (qb, kb, vb, c["pmap"], z, m, c["block_m"], c["block_n"], c["bnm"], c["scale"])
+            d16 = np.abs(got - _oracle_sub_block(*args, "fp32_k16"))
+            dex = np.abs(got - _oracle_sub_block(*args, "exact"))
+            within = float((dex <= 2e-3).mean())
+            line.append(f"({z},{m}) k16 {d16.max():.2e}/{d16.mean():.1e} exact {dex.max():.2e}/{dex.mean():.1e} "
+                        f"{within:.5f}")
+            worst["k16_max"] = max(worst["k16_max"], d16.max())
+            worst["k16_mean"] = max(worst["k16_mean"], d16.mean())
+            worst["exact_max"] = max(worst["exact_max"], dex.max())
+            worst["exact_mean"] = max(worst["exact_mean"], dex.mean())
+            worst["exact_within"] = min(worst["exact_within"], within)
+            assert d16.max() <= 2e-3 and d16.mean() <= 2e-4, (layer, z, m, d16.max(), d16.mean())
+            assert dex.mean() <= 2e-4 and within >= 0.999, (layer, z, m, dex.mean(), within)
+        print(f"cfg5 layer {layer:2d}: " + "; ".join(line), flush=True)
+    print("cfg5 per-layer worst: " + ", ".join(f"{k} {v:.3e}" for k, v in worst.items()), flush=True)
+
+
 @pytest.mark.timeout(900)
 def test_cfg5_top1_agrees_with_oracle_attention(device, cfg5_model, monkeypatch):
     """Top-1 of TileMix vs the oracle-attention model, beside a control: the same
@@ -80,7 +172,7 @@ def test_cfg5_top1_agrees_with_oracle_attention(device, cfg5_model, monkeypatch)
     oracle's semantics."""
     model = cfg5_model
     vocab = model.config.vocab_size
-    ids = torch.randint(100, vocab, (8, 256), generator=torch.Generator().manual_seed(1)).to(device)
+    ids = torch.randint(100, vocab, (12, 256), generator=torch.Generator().manual_seed(1)).to(device)
 
     def run_with(accum):
         calls = []
@@ -121,10 +213,18 @@ def test_cfg5_top1_agrees_with_oracle_attention(device, cfg5_model, monkeypatch)
           flush=True)
     agree, last, dmax, dmean = res["tilemix_vs_oracle"]
     c_agree, _, c_dmax, c_dmean = res["control_oracle_vs_oracle_fp32k16"]
-    # Measured on MI355X: agreement 0.9873 vs the control's 0.9902, logits
-    # mean-abs 6.2e-3 vs 5.0e-3 (2048 positions; the standard error of either
-    # agreement is ~0.0022).
-    assert agree >= 0.999 or agree >= c_agree - 0.005, (agree, c_agree)
+    # Oracle-stable positions: the two valid oracle models give the same top-1.
+    t_got, t_ref, t_ref32 = got.argmax(-1), ref.argmax(-1), ref32.argmax(-1)
+    stable = t_ref == t_ref32
+    n_stable = int(stable.sum().item())
+    agree_stable = (t_got == t_ref)[stable].float().mean().item()
+    print(f"cfg5 top-1 on oracle-stable positions: {agree_stable:.5f} over {n_stable} positions "
+          f"(all positions {agree:.5f})", flush=True)
+    assert n_stable >= 2048, n_stable
+    assert agree_stable >= 0.999, (agree_stable, n_stable)
+    # Fixed floor on the all-position rate (measured 0.9873 over 2048 positions
+    # of this model; the control of two oracle models measured 0.9902).
+    assert agree >= 0.98, agree
     assert dmean <= 1.5 * c_dmean, (dmean, c_dmean)
     # every position whose top-2 gap is wider than three times the largest
     # logit difference of the control agrees

@@ -99,6 +99,39 @@ def test_llama_forced_block_n(device, monkeypatch, forced):
     assert diff.max().item() < 0.05 and diff.mean().item() < 2e-3
 
 
+@pytest.mark.parametrize("forced", ["256,64", "512,64"])
+def test_llama_forced_block_m_fallback(device, monkeypatch, forced):
+    """TILEMIX_FORCE_CONFIG at a sequence shorter than every available block_n
+    (40 tokens): the reference falls back to the nearest of block_m 64 / 128 /
+    256 / 512 (models/tilemix_llama.py:137-140), here 256 or 512, and the model
+    runs it and agrees with the oracle attention of that block_m."""
+    monkeypatch.setenv("TILEMIX_FORCE_CONFIG", forced)
+    cfg = LlamaConfig(vocab_size=512, hidden_size=256, intermediate_size=512, num_hidden_layers=2,
+                      num_attention_heads=4, num_key_value_heads=2, rope_theta=500000.0)
+    torch.manual_seed(11)
+    model = LlamaForCausalLM(cfg).half().to(device).eval()
+    TL.inject_tilemix_into_llama(model)
+    TL.configure_tilemix_attention_pattern(model, "sptrans", percentage=0.5, stride=128, c=32)
+    seen = []
+    real = TL.tilemix_varlen_attention
+
+    def spy(q, k, v, block_m, block_n, **kw):
+        seen.append((block_m, block_n))
+        return real(q, k, v, block_m, block_n, **kw)
+
+    ids = torch.randint(0, 512, (4, 40), generator=torch.Generator().manual_seed(12)).to(device)
+    with torch.no_grad():
+        monkeypatch.setattr(TL, "tilemix_varlen_attention", spy)
+        got = model(ids).logits.float()
+        monkeypatch.setattr(TL, "tilemix_varlen_attention", _oracle_varlen_attention)
+        ref = model(ids).logits.float()
+    assert set(seen) == {tuple(int(x) for x in forced.split(","))}
+    agree = (got.argmax(-1) == ref.argmax(-1)).float().mean().item()
+    diff = (got - ref).abs()
+    assert agree >= 0.999, agree
+    assert diff.max().item() < 0.05 and diff.mean().item() < 2e-3
+
+
 def test_llama_head_dim_72(device, monkeypatch):
     """A head_dim that is not a multiple of 16 (72): the host zero-pads Q/K/V
     and the model agrees with the oracle attention at the original width."""

@@ -9,7 +9,10 @@
   through the score dump;
 * head_dims that are not multiples of 16 (24, 40, 72, 100, 120, 127): the
   host layer zero-pads Q/K/V to the next multiple of 16, the reference masks
-  the columns past head_dim (:252, :364, :639).
+  the columns past head_dim (:252, :364, :639);
+* block_m 256 and 512 (the reference's fallback sizes), bias on the GEN
+  kernels, and Q/K/V views whose strides exceed the kernel's 2 GiB buffer
+  span.
 
 All against the CPU oracle at the full bar (max-abs 2e-3, mean-abs 2e-4).
 """
@@ -29,17 +32,19 @@ MODES = {"mixed": 0, "fp16": 1, "int8": 2}
 
 
 def _case(device, lengths, hq, hk, d, block_m, block_n, bnm, causal, mode, int8v, seed, blkk=64, blkq=128,
-          outliers=()):
+          outliers=(), bias=None):
     """Launch through tilemix_attention_with_quant and run the oracle on the same inputs."""
     q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=seed, outliers=outliers)
     max_len = max(lengths)
     bits = random_bitmask(hk, -(-max_len // block_m), seed)
     print(f"case lengths={lengths} hq={hq} hk={hk} d={d} block_m={block_m} block_n={block_n} bnm={bnm} "
-          f"causal={causal} mode={mode} int8_use_fp16_v={int8v} BLKK={blkk} seed={seed}", flush=True)
+          f"causal={causal} mode={mode} int8_use_fp16_v={int8v} BLKK={blkk} seed={seed} "
+          f"bias={bias is not None}", flush=True)
     out, mode_ret = tmx.tilemix_attention_with_quant(
         to_dev(q, device), to_dev(k, device), to_dev(v, device), to_dev(cu, device), to_dev(cu, device),
         max_len, max_len, bitmask_tensor(bits, device), block_m=block_m, block_n=block_n, block_n_mask=bnm,
-        BLKQ=blkq, BLKK=blkk, causal=causal, routing_mode=mode, scalar_scales=False, int8_use_fp16_v=int8v)
+        BLKQ=blkq, BLKK=blkk, causal=causal, routing_mode=mode, scalar_scales=False, int8_use_fp16_v=int8v,
+        bias=None if bias is None else to_dev(bias, device))
     torch.cuda.synchronize()
     assert mode_ret == mode
     q8, sq, cuq = O.quant_per_block_int8(q, cu, blkq)
@@ -51,7 +56,7 @@ def _case(device, lengths, hq, hk, d, block_m, block_n, bnm, causal, mode, int8v
     ref = O.attn_fwd(q, k, v, cu, cu, bits, block_m=block_m, block_n_mask=bnm, causal=causal,
                      routing_mode=MODES[mode], q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
                      cu_q_scale=cuq, cu_k_scale=cuk, blkq=blkq, blkk=blkk, int8_use_fp16_v=int8v,
-                     block_n=block_n, **extra)
+                     block_n=block_n, bias=bias, **extra)
     return out.cpu().numpy(), ref
 
 
@@ -92,6 +97,111 @@ def test_block_n_changes_the_result(device):
     assert_close_out(got128, ref128)
     assert not np.array_equal(ref64, ref128)
     assert not np.array_equal(got64, got128)
+
+
+# block_m 256 / 512 (the reference's fallback sizes, models/tilemix_llama.py:137-140,
+# launched with the fallback config, attention/triton/tilemix.py:1074-1084): 128-row
+# workgroups that read the routing row of the block holding them.
+# name, lengths, hq, hk, d, block_m, block_n, block_n_mask, causal, mode, int8_use_fp16_v
+BLOCK_M_LARGE_CASES = [
+    ("bm256_mixed", [700, 129, 1], 4, 2, 128, 256, 64, 64, True, "mixed", True),
+    ("bm512_mixed", [1200, 300], 4, 2, 128, 512, 64, 128, True, "mixed", True),
+    ("bm256_mixed_int8v", [700, 200], 4, 2, 128, 256, 64, 64, True, "mixed", False),
+    ("bm512_mixed_int8v_d64", [900], 4, 1, 64, 512, 64, 64, True, "mixed", False),
+    ("bm256_bn128_mixed", [600, 77], 4, 2, 128, 256, 128, 256, True, "mixed", True),
+    ("bm256_int8", [333], 4, 2, 128, 256, 64, 64, True, "int8", True),
+    ("bm512_noncausal", [520, 40], 2, 1, 128, 512, 64, 64, False, "mixed", True),
+]
+
+
+@pytest.mark.parametrize("case", BLOCK_M_LARGE_CASES, ids=[c[0] for c in BLOCK_M_LARGE_CASES])
+def test_block_m_256_512_matches_oracle(device, case):
+    name, lengths, hq, hk, d, block_m, block_n, bnm, causal, mode, int8v = case
+    got, ref = _case(device, lengths, hq, hk, d, block_m, block_n, bnm, causal, mode, int8v, seed=57)
+    assert_close_out(got, ref)
+
+
+def test_block_m_256_reads_its_blocks_routing_row(device):
+    """block_m 256 and 128 on the same inputs and one routing pattern per
+    256 rows: the block_m 256 launch with map row j equals the block_m 128
+    launch whose rows 2j and 2j + 1 both hold row j (bit for bit), and differs
+    from one that takes the rows unexpanded."""
+    lengths, hq, hk, d = [700], 4, 2, 128
+    q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=58)
+    bits256 = random_bitmask(hk, 3, 58)
+    bits128 = np.repeat(bits256.reshape(hk, 3), 2, axis=1)[:, :6].reshape(-1)
+    dev = lambda a: to_dev(a, device)  # noqa: E731
+    outs = {}
+    for name, bm, bits in (("256", 256, bits256), ("128", 128, bits128),
+                           ("128_unexpanded", 128, np.resize(bits256, hk * 6))):
+        outs[name], _ = tmx.tilemix_attention_with_quant(
+            dev(q), dev(k), dev(v), dev(cu), dev(cu), 700, 700, bitmask_tensor(bits, device), block_m=bm,
+            block_n=64, causal=True, routing_mode="mixed", scalar_scales=False, int8_use_fp16_v=True)
+    torch.cuda.synchronize()
+    assert torch.equal(outs["256"], outs["128"])
+    assert not torch.equal(outs["256"], outs["128_unexpanded"])
+
+
+# Bias on the GEN kernels (block_n 128 / 256, or BLKK not a multiple of 64):
+# the masked max pass and the update pass both add it.
+# name, lengths, hq, hk, d, block_m, block_n, block_n_mask, mode, int8_use_fp16_v, BLKK
+GEN_BIAS_CASES = [
+    ("bn128_mixed_bm128", [300, 129], 4, 2, 128, 128, 128, 128, "mixed", True, 64),
+    ("bn256_mixed_bm64_int8v", [400, 100], 4, 2, 128, 64, 256, 256, "mixed", False, 64),
+    ("bn128_mixed_bm64_split", [333, 64], 4, 2, 128, 64, 128, 128, "mixed", True, 64),
+    ("blkk32_int8_bm128_int8v", [300], 4, 2, 128, 128, 64, 128, "int8", False, 32),
+    ("blkk32_bn128_mixed_bm64_int8v", [333, 64], 4, 2, 128, 64, 128, 128, "mixed", False, 32),
+    ("bn256_fp16_bm128_d64", [520], 2, 1, 64, 128, 256, 256, "fp16", True, 64),
+]
+
+
+@pytest.mark.parametrize("case", GEN_BIAS_CASES, ids=[c[0] for c in GEN_BIAS_CASES])
+def test_gen_bias_matches_oracle(device, case):
+    """Additive fp16 bias (reference :264-272, batch-0 bias for every sequence)
+    through the GEN kernels, fp16 and int8 V, against the oracle."""
+    name, lengths, hq, hk, d, block_m, block_n, bnm, mode, int8v, blkk = case
+    rng = np.random.default_rng(59)
+    bias = (rng.standard_normal((len(lengths), hq, max(lengths), max(lengths))) * 2).astype(np.float16)
+    got, ref = _case(device, lengths, hq, hk, d, block_m, block_n, bnm, True, mode, int8v, seed=59, blkk=blkk,
+                     bias=bias)
+    assert_close_out(got, ref)
+
+
+def test_kv_span_beyond_2gib(device):
+    """Q, K and V as views into one buffer with a 16 MiB token stride: (max_seqlen_k
+    + 64) K/V token strides and 128 Q token strides exceed the kernel's 2 GiB
+    buffer span, so the host passes head-major copies (token stride head_dim).
+    The output equals the launch on dense copies bit for bit and matches the
+    oracle (the reference addresses any strides with 64-bit pointers,
+    attention/triton/tilemix.py:1259-1275)."""
+    lengths, hq, hk, d = [300, 129], 4, 2, 128
+    q, k, v, cu = packed_inputs(lengths, hq, hk, d, seed=60)
+    n = sum(lengths)
+    stride = 8 << 20  # elements per token: 16 MiB
+    buf = torch.empty((n, stride), dtype=torch.float16, device=device)
+    cols = [(0, hq), (hq, hk), (hq + hk, hk)]
+    views = [buf.as_strided((n, h, d), (stride, d, 1), c0 * d) for c0, h in cols]
+    for view, a in zip(views, (q, k, v)):
+        view.copy_(to_dev(a, device))
+    qv, kv, vv = views
+    assert not tmx._span_fits(kv, 300 + 64) and not tmx._span_fits(qv, 128)
+    max_len = max(lengths)
+    bits = random_bitmask(hk, -(-max_len // 128), 60)
+    print(f"span case lengths={lengths} token stride={stride * 2} bytes", flush=True)
+    kw = dict(block_m=128, block_n=64, causal=True, routing_mode="mixed", scalar_scales=True,
+              int8_use_fp16_v=True)
+    cud, bmd = to_dev(cu, device), bitmask_tensor(bits, device)
+    out_view, _ = tmx.tilemix_attention_with_quant(qv, kv, vv, cud, cud, max_len, max_len, bmd, **kw)
+    out_dense, _ = tmx.tilemix_attention_with_quant(qv.contiguous(), kv.contiguous(), vv.contiguous(), cud, cud,
+                                                    max_len, max_len, bmd, **kw)
+    torch.cuda.synchronize()
+    del buf, views, qv, kv, vv
+    assert torch.equal(out_view, out_dense)
+    q8, sq, cuq = O.quant_per_block_int8(q, cu, 128)
+    k8, sk, cuk = O.quant_per_block_int8(k, cu, 64)
+    ref = O.attn_fwd(q, k, v, cu, cu, bits, block_m=128, block_n_mask=64, causal=True, q8=q8, k8=k8,
+                     sq16=sq.astype(np.float16), sk16=sk.astype(np.float16), cu_q_scale=cuq, cu_k_scale=cuk)
+    assert_close_out(out_view.cpu().numpy(), ref)
 
 
 # name, lengths, hq, hk, d, block_m, block_n, mode, int8_use_fp16_v, BLKK

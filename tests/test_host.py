@@ -239,6 +239,42 @@ def test_launch_requires_gpu_tensors():
                                          routing_mode="mixed")
 
 
+def test_mismatched_head_dims_are_rejected_before_padding(monkeypatch):
+    """q with head_dim 72 and k/v with 64 (or K != V): the reference's
+    ValueError, raised before the head-dim padding (which would pad all three
+    to 80 and let them pass) and before any launch."""
+    calls = []
+    monkeypatch.setattr(tmx, "launch_prequantized", lambda *a, **kw: calls.append(1))
+    cu = torch.tensor([0, 64], dtype=torch.int32)
+    bm = torch.zeros(1, dtype=torch.uint64)
+    q = torch.zeros(64, 2, 72, dtype=torch.float16)
+    k = torch.zeros(64, 1, 64, dtype=torch.float16)
+    kw = dict(block_m=64, block_n=64, causal=True, routing_mode="fp16")
+    with pytest.raises(ValueError, match="K/V shapes and Q/K/V head dimensions must match"):
+        tmx.tilemix_attention_with_quant(q, k, k, cu, cu, 64, 64, bm, **kw)
+    with pytest.raises(ValueError, match="K/V shapes and Q/K/V head dimensions must match"):
+        tmx.tilemix_attention_with_quant(q, q[:, :1], q[:, :1, :64], cu, cu, 64, 64, bm, **kw)
+    with pytest.raises(ValueError, match="expected flattened"):
+        tmx.tilemix_attention_with_quant(q[None], k, k, cu, cu, 64, 64, bm, **kw)
+    assert not calls
+
+
+def test_wide_token_strides_get_a_head_major_copy():
+    """The kernel reads (max_seqlen_k + 64) K/V token strides (and 128 Q token
+    strides) through one 32-bit buffer: a view whose span reaches 2 GiB is
+    replaced by a head-major copy of the same values (token stride head_dim),
+    any other tensor is passed through as is."""
+    small = torch.zeros(10, 2, 16, dtype=torch.float16)
+    assert tmx._token_stride_fit(small, 1000) is small
+    base = torch.arange(4 * (1 << 20), dtype=torch.float16).view(4, 1 << 20)
+    view = base.as_strided((4, 2, 16), (1 << 20, 16, 1), 32)  # 2 MiB token stride
+    assert not tmx._span_fits(view, 1024)
+    fit = tmx._token_stride_fit(view, 1024)
+    assert fit.stride() == (16, 64, 1) and torch.equal(fit, view)
+    assert tmx._span_fits(fit, 1024)
+    assert tmx._token_stride_fit(view, 1000) is view  # 1000 rows of 2 MiB stay below 2 GiB
+
+
 def test_varlen_entry_validates_before_launch():
     q = torch.zeros(1, 4, 256, 64, dtype=torch.float16)
     k = torch.zeros(1, 1, 256, 64, dtype=torch.float16)

@@ -12,14 +12,23 @@ its formula:
 * attention at an all-FP16 map: fp64 softmax(QK^T)V within fp16 rounding,
   including Lq != Lk (causal offset), GQA and varlen packing;
 * INT8 route: fp64 attention over the dequantised scores;
+* INT8 route on int8 V codes: fp64 attention over the dequantised scores and
+  the dequantised V (BLKK 64 and 16), and a hand-derived known answer in which
+  the fp16 rounding of p * sv changes the output;
+* bias: a hand-derived known answer in which LOG2E taken at fp16 changes a
+  score, fp64 attention over scores plus bias, and the batch-0 reading of the
+  bias in a two-sequence launch;
 * one 64-key tile: brute force of the online-softmax update;
 * routing rows / bits: per-element bit extraction.
 
 A mutation harness then re-executes the oracle's own source with one planted
 mistake at a time (wrong causal offset, dropped 1/l, wrong GQA head map,
 wrong route bit, round-half-even instead of half-away, missing softmax scale
-in the INT8 dequant, inverted alpha) and requires every mutant to fail at
-least one of the checks above.  Everything runs on the CPU.
+in the INT8 dequant, inverted alpha, softmax steps of 64 keys, K scale blocks
+of 64, the V scale dropped, fp16 V on INT8 tiles, p * sv unrounded, the bias's
+LOG2E dropped or taken in fp32, a per-sequence or transposed bias) and
+requires every mutant to fail at least one of the checks above.  Everything
+runs on the CPU.
 """
 from __future__ import annotations
 
@@ -296,6 +305,161 @@ def check_int8_vector_scales(Om):
         assert err.max() < 4e-3 and err.mean() < 4e-4, (blkk, err.max(), err.mean())
 
 
+def _int8_v_setup(seed, blkk):
+    """INT8-route inputs with int8 V codes: V ~ 4 N(0,1), so one code step
+    (~0.11) is far above the output tolerance."""
+    q, k, v, cu_q, cu_k = _inputs([150, 70], 4, 2, 64, seed=seed)
+    v = (v.astype(f32) * 4).astype(f16)
+    q8, sq, cuq = O.quant_per_block_int8(q, cu_q, 128)
+    k8, sk, cuk = O.quant_per_block_int8(k, cu_k, blkk)
+    v8, sv, cuv = O.quant_per_block_int8(v, cu_k, blkk)
+    return q, k, v, cu_q, cu_k, q8, sq.astype(f16), cuq, k8, sk.astype(f16), cuk, v8, sv.astype(f16), cuv
+
+
+def check_int8_v_attention(Om):
+    """INT8 route on int8 V codes (reference :449-497, INT8_USE_FP16_V = 0):
+    fp64 attention over the dequantised scores and the dequantised V
+    (v8 * sv of the key's BLKK block), with BLKK 64 (one V scale per tile,
+    :472-481) and 16 (per-key V scales, :483-495).  Using the fp16 V in place of
+    the codes moves the outputs by the V quantisation error (~0.05)."""
+    for blkk in (64, 16):
+        q, k, v, cu_q, cu_k, q8, sq16, cuq, k8, sk16, cuk, v8, sv16, cuv = _int8_v_setup(19, blkk)
+        out = Om.attn_fwd(q, k, v, cu_q, cu_k, _all_bits(2, 3, ~np.uint64(0)), block_m=64, block_n_mask=64,
+                          causal=True, routing_mode=O.ROUTING_INT8, q8=q8, k8=k8, sq16=sq16, sk16=sk16,
+                          cu_q_scale=cuq, cu_k_scale=cuk, blkk=blkk, int8_use_fp16_v=False,
+                          v8=v8, sv16=sv16, cu_v_scale=cuv)
+
+        def scores(z, h):
+            qa = q8[cu_q[z]:cu_q[z + 1], h].astype(np.float64)
+            ka = k8[cu_k[z]:cu_k[z + 1], h // 2].astype(np.float64)
+            lq, lk = qa.shape[0], ka.shape[0]
+            rq = sq16[cuq[z] + np.arange(lq) // 128, h].astype(np.float64)
+            rk = sk16[cuk[z] + np.arange(lk) // blkk, h // 2].astype(np.float64)
+            return (qa @ ka.T) * rq[:, None] * rk[None, :] * 64 ** -0.5
+
+        vdq = np.zeros(v.shape, np.float64)
+        for z in range(2):
+            for hk in range(2):
+                keys = np.arange(cu_k[z + 1] - cu_k[z])
+                s = sv16[cuv[z] + keys // blkk, hk].astype(np.float64)
+                vdq[cu_k[z]:cu_k[z + 1], hk] = v8[cu_k[z]:cu_k[z + 1], hk].astype(np.float64) * s[:, None]
+        ref = _fp64_attention(q, k, vdq, cu_q, cu_k, True, scores=scores)
+        err = np.abs(out.astype(np.float64) - ref)
+        # The bars of check_int8_attention scaled by the V magnitude (x4).
+        assert err.max() < 1.6e-2 and err.mean() < 1.6e-3, (blkk, err.max(), err.mean())
+
+
+def check_int8_v_known_answer(Om):
+    """One row, two keys with given scores 0 and -s on the INT8 route with int8 V
+    codes 0 and 100 (column 0) and V scale sv: m = 0, p0 = 1, p1 = fp16(2^-s),
+    l = 1 + p1 (the row sum takes p, not p * sv), and PV takes p scaled in fp16
+    (:472-481): out = fp16(fp16(p1 sv) 100 / (1 + p1)).  (s, sv) is the first
+    pair of a fixed list for which leaving p sv unrounded gives another output."""
+    L, d = 2, 16
+    zeros8 = np.zeros((L, 1, d), np.int8)
+    z16 = np.zeros((L, 1, d), f16)
+    v8 = np.zeros((L, 1, d), np.int8)
+    v8[1, 0, 0] = 100
+    one = np.ones((1, 1), f16)
+    cu = np.array([0, L])
+    choice = None
+    for s in (0.5, 0.75, 1.25, 1.5, 2.5):
+        p1 = f32(f16(np.exp2(f32(-s))))
+        for sv in (0.3, 0.37, 0.41, 0.53, 0.61, 0.77, 0.9):
+            sv16 = f32(f16(sv))
+            den = f32(f32(1) + p1)
+            rounded = f16(f32(f32(f16(p1 * sv16)) * f32(100)) / den)
+            unrounded = f16(f32(f32(p1 * sv16) * f32(100)) / den)
+            if rounded != unrounded:
+                choice = (s, sv, rounded)
+                break
+        if choice:
+            break
+    assert choice is not None
+    s, sv, want = choice
+    sc = np.array([[0.0, -s], [0.0, -s]], f16)
+    out = Om.attn_fwd(z16, z16, z16, cu, cu, _all_bits(1, 1, 1), block_m=64, block_n_mask=64, causal=False,
+                      routing_mode=O.ROUTING_INT8, q8=zeros8, k8=zeros8, sq16=one, sk16=one,
+                      cu_q_scale=np.array([0, 1]), cu_k_scale=np.array([0, 1]), int8_use_fp16_v=False,
+                      v8=v8, sv16=np.array([[sv]], f16), cu_v_scale=np.array([0, 1]),
+                      qk16_override=lambda z, h: sc)
+    assert out[0, 0, 0] == want and out[1, 0, 0] == want, (out[:, 0, 0], want, s, sv)
+
+
+def check_bias_known_answer(Om):
+    """One row, two keys with given fp16 scores 14.4375 and 0, bias 0 and 10,
+    V = [0, 1] (column 0).  Reference :264-272: qk += fp16(b * LOG2E), where the
+    fp16 bias times the Python constant computes in fp16, i.e. with LOG2E
+    rounded to fp16 (1.4423828125): key 1's score is fp16(10 * 1.4423828125) =
+    14.421875 (an fp32 LOG2E would give 14.4296875).  m = 14.4375, p0 = 1,
+    p1 = fp16(2^(14.421875 - 14.4375)), out = fp16(p1 / (1 + p1))."""
+    L, d = 2, 16
+    z16 = np.zeros((L, 1, d), f16)
+    v = np.zeros((L, 1, d), f16)
+    v[1, 0, 0] = 1
+    cu = np.array([0, L])
+    sc = np.array([[14.4375, 0.0], [14.4375, 0.0]], f16)
+    bias = np.zeros((1, 1, L, L), f16)
+    bias[0, 0, :, 1] = 10
+    assert f16(10 * f16(O.LOG2E)) == f16(14.421875) and f16(10 * O.LOG2E) == f16(14.4296875)
+    p1 = f16(np.exp2(f32(f32(14.421875) - f32(14.4375))))
+    want = f16(f32(p1) / f32(f32(1) + f32(p1)))
+    out = Om.attn_fwd(z16, z16, v, cu, cu, _all_bits(1, 1, 0), block_m=64, block_n_mask=64, causal=False,
+                      qk16_override=lambda z, h: sc, bias=bias)
+    assert out[0, 0, 0] == want and out[1, 0, 0] == want, (out[:, 0, 0], want)
+
+
+def check_bias_attention(Om):
+    """Random bias on a causal GQA launch at both routes: fp64 softmax(q k^T sm +
+    bias) v (a bias b in natural-log units is b * LOG2E in the kernel's base-2
+    scores), within fp16 rounding of the bias term and the scores."""
+    q, k, v, cu_q, cu_k = _inputs([96], 4, 2, 64, seed=23)
+    rng = np.random.default_rng(29)
+    bias = (rng.standard_normal((1, 4, 96, 96)) * 2).astype(f16)
+    bias[0, :, 5, :] = 0
+    q8, sq, cuq = O.quant_per_block_int8(q, cu_q, 128)
+    k8, sk, cuk = O.quant_per_block_int8(k, cu_k, 64)
+    sq16, sk16 = sq.astype(f16), sk.astype(f16)
+    for mode in (O.ROUTING_FP16, O.ROUTING_INT8):
+        out = Om.attn_fwd(q, k, v, cu_q, cu_k, _all_bits(2, 2, 0), block_m=64, block_n_mask=64, causal=True,
+                          routing_mode=mode, q8=q8, k8=k8, sq16=sq16, sk16=sk16, cu_q_scale=cuq,
+                          cu_k_scale=cuk, bias=bias)
+
+        def scores(z, h):
+            if mode == O.ROUTING_FP16:
+                s = q[:, h].astype(np.float64) @ k[:, h // 2].astype(np.float64).T * 64 ** -0.5
+            else:
+                s = (q8[:, h].astype(np.float64) @ k8[:, h // 2].astype(np.float64).T
+                     * sq16[0, h].astype(np.float64) * sk16[np.arange(96) // 64, h // 2].astype(np.float64)[None, :]
+                     * 64 ** -0.5)
+            return s + bias[0, h].astype(np.float64)
+
+        ref = _fp64_attention(q, k, v, cu_q, cu_k, True, scores=scores)
+        err = np.abs(out.astype(np.float64) - ref)
+        assert err.max() < 1e-2 and err.mean() < 1e-3, (mode, err.max(), err.mean())
+
+
+def check_bias_batch0(Om):
+    """The reference reads the bias without a batch offset (:264-272: the
+    pointer takes head, row and key strides, never stride_bz): every sequence of
+    a packed launch adds bias[0].  Two sequences of 40 and 56 tokens: the second
+    sequence's rows equal a launch of that sequence alone with bias[0], and
+    differ from one with bias[1]."""
+    q, k, v, cu_q, cu_k = _inputs([40, 56], 2, 1, 32, seed=31)
+    rng = np.random.default_rng(37)
+    bias = (rng.standard_normal((2, 2, 56, 56)) * 3).astype(f16)
+    out = Om.attn_fwd(q, k, v, cu_q, cu_k, _all_bits(1, 1, 0), block_m=64, block_n_mask=64, causal=True,
+                      bias=bias)
+    cu1 = np.array([0, 56])
+    sl = slice(40, 96)
+    alone0 = Om.attn_fwd(q[sl], k[sl], v[sl], cu1, cu1, _all_bits(1, 1, 0), block_m=64, block_n_mask=64,
+                         causal=True, bias=bias[:1])
+    alone1 = Om.attn_fwd(q[sl], k[sl], v[sl], cu1, cu1, _all_bits(1, 1, 0), block_m=64, block_n_mask=64,
+                         causal=True, bias=bias[1:])
+    assert np.array_equal(out[sl], alone0)
+    assert not np.array_equal(out[sl], alone1)
+
+
 def check_route_table(Om):
     rng = np.random.default_rng(2)
     bm = rng.integers(0, 2 ** 63, size=3 * 4, dtype=np.uint64) * np.uint64(2) + np.uint64(1)
@@ -311,7 +475,8 @@ def check_route_table(Om):
 CHECKS = [check_quant_invariants, check_quant_halfway, check_quant_bruteforce, check_quant_zero_and_tail,
           check_int32_accumulators, check_fp16_attention, check_int8_attention, check_single_tile,
           check_single_tile_block_n256, check_block_n_known_answer, check_block_n_fp16_attention,
-          check_int8_vector_scales, check_route_table]
+          check_int8_vector_scales, check_int8_v_attention, check_int8_v_known_answer, check_bias_known_answer,
+          check_bias_attention, check_bias_batch0, check_route_table]
 
 
 @pytest.mark.parametrize("check", CHECKS, ids=[c.__name__ for c in CHECKS])
@@ -334,6 +499,17 @@ MUTATIONS = {
                         ("k0, k1 = n * block_n, min((n + 1) * block_n, Lk)", "k0, k1 = n * BN, min((n + 1) * BN, Lk)")],
     "k_scale_block_64": ("int(cu_k_scale[z + 1]),\n                                 keys // blkk",
                          "int(cu_k_scale[z + 1]),\n                                 keys // 64"),
+    # int8 V codes: the V scale dropped, fp16 V used on INT8 tiles, p * sv left unrounded
+    "int8v_no_sv": ("p_sc = (p16.astype(f32) * sv[None, k0:k1].astype(f32)).astype(f16)", "p_sc = p16"),
+    "int8v_fp16_v": ("pv8 = (p_sc.astype(f32) @ v8h[k0:k1])", "pv8 = (p_sc.astype(f32) @ vh[k0:k1])"),
+    "int8v_unrounded_p_sv": ("p_sc = (p16.astype(f32) * sv[None, k0:k1].astype(f32)).astype(f16)",
+                             "p_sc = (p16.astype(f32) * sv[None, k0:k1].astype(f32))"),
+    # bias: LOG2E factor dropped, LOG2E taken in fp32, per-sequence bias, transposed bias
+    "bias_no_log2e": ("bl = (b.astype(f32) * f32(f16(LOG2E))).astype(f16)", "bl = b"),
+    "bias_fp32_log2e": ("bl = (b.astype(f32) * f32(f16(LOG2E))).astype(f16)",
+                        "bl = (b.astype(f32) * f32(LOG2E)).astype(f16)"),
+    "bias_batch_offset": ("np.asarray(bias)[0, h, :Lq, :Lk]", "np.asarray(bias)[min(z, len(bias) - 1), h, :Lq, :Lk]"),
+    "bias_transposed": ("np.asarray(bias)[0, h, :Lq, :Lk]", "np.asarray(bias)[0, h, :Lk, :Lq].T"),
 }
 
 

@@ -48,7 +48,7 @@ RoutingMode = Literal["auto", "mixed", "fp16", "int8"]
 
 # Tile sizes the gfx950 kernel is instantiated for (block_n > 64 runs as
 # 64-key tiles with the reference's per-block_n softmax step).
-SUPPORTED_BLOCK_M = (64, 128)
+SUPPORTED_BLOCK_M = (64, 128, 256, 512)
 SUPPORTED_BLOCK_N = (64, 128, 256)
 # The kernel's head-dim granularity; other widths are zero-padded to it.
 HEAD_DIM_MULTIPLE = 16
@@ -204,6 +204,26 @@ def _inner_contiguous(t: torch.Tensor, align: int) -> torch.Tensor:
     return t
 
 
+# The kernel reads a sequence's K/V tiles through 32-bit buffer offsets:
+# (max_seqlen_k + 64) * token stride must stay below 2 GiB, and 128 Q rows
+# likewise (include/tilemix_hip.h).
+_SPAN_LIMIT = 1 << 31
+
+
+def _span_fits(t: torch.Tensor, rows: int) -> bool:
+    return rows * t.stride(0) * t.element_size() < _SPAN_LIMIT
+
+
+def _token_stride_fit(t: torch.Tensor, rows: int) -> torch.Tensor:
+    """``t`` itself when ``rows`` token strides span less than 2 GiB, else a
+    head-major copy: the same [tokens, heads, d] tensor with token stride d,
+    so the span becomes rows * d elements (the reference addresses K/V with
+    64-bit pointers over any strides, attention/triton/tilemix.py:1259-1275)."""
+    if _span_fits(t, rows):
+        return t
+    return t.transpose(0, 1).contiguous().transpose(0, 1)
+
+
 @torch.no_grad()
 def launch_prequantized(
     q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
@@ -272,7 +292,7 @@ def launch_prequantized(
     q_in_kernel = bool(_q_in_kernel) and mode_code != ROUTING_MODE_FP16
     if q_in_kernel and not _q_in_kernel_supported(block_m, BLKQ, mode_code, int8_use_fp16_v):
         raise ValueError("in-kernel Q quantisation needs BLKQ == 128 and 128-row workgroups "
-                         "(block_m 128, or block_m 64 without mixed routing on int8 V codes)")
+                         "(block_m 128, 256 or 512, or block_m 64 without mixed routing on int8 V codes)")
     if mode_code != ROUTING_MODE_FP16 and not q_in_kernel and (q8 is None or sQ_blocks is None
                                                                 or cu_q_scale is None):
         raise ValueError("q8, sQ_blocks and cu_q_scale are required")
@@ -304,9 +324,10 @@ def launch_prequantized(
     if run_dim != head_dim:
         q, k, v = (_pad_head_dim(t, run_dim) for t in (q, k, v))
         q8, k8, v8 = (_pad_head_dim(t, run_dim) for t in (q8, k8, v8))
-    q = _inner_contiguous(q, 8)
-    k = _inner_contiguous(k, 8)
-    v = _inner_contiguous(v, 8)
+    kv_rows = int(max_seqlens_k) + 64
+    q = _token_stride_fit(_inner_contiguous(q, 8), 128)
+    k = _token_stride_fit(_inner_contiguous(k, 8), kv_rows)
+    v = _token_stride_fit(_inner_contiguous(v, 8), kv_rows)
     o_dev = o if (run_dim == head_dim and o.stride(2) == 1 and o.stride(0) % 4 == 0 and o.stride(1) % 4 == 0
                   and o.data_ptr() % 8 == 0) else torch.empty(q.shape, dtype=q.dtype, device=q.device)
     device = q.device
@@ -335,14 +356,14 @@ def launch_prequantized(
             keep += [q8c, sq, cqs]
             p.q8, p.sq, p.cu_q_scale = q8c.data_ptr(), sq.data_ptr(), cqs.data_ptr()
             p.stride_q8_token, p.stride_q8_head = q8c.stride(0), q8c.stride(1)
-        k8c = _inner_contiguous(k8, 16)
+        k8c = _token_stride_fit(_inner_contiguous(k8, 16), kv_rows)
         sk = sK_blocks.to(torch.float16).contiguous()
         cks = cu_k_scale.to(dtype=torch.int32).contiguous()
         keep += [k8c, sk, cks]
         p.k8, p.sk, p.cu_k_scale = k8c.data_ptr(), sk.data_ptr(), cks.data_ptr()
         p.stride_k8_token, p.stride_k8_head = k8c.stride(0), k8c.stride(1)
         if not int8_use_fp16_v:
-            v8c = _inner_contiguous(v8, 16)
+            v8c = _token_stride_fit(_inner_contiguous(v8, 16), kv_rows)
             sv = sV_blocks.to(torch.float16).contiguous()
             cvs = cu_v_scale.to(dtype=torch.int32).contiguous()
             keep += [v8c, sv, cvs]
@@ -394,9 +415,16 @@ def tilemix_attention_with_quant(
     """
     if block_n_mask is None:
         block_n_mask = block_n
+    # launch_prequantized's shape checks (reference :1169-1172), before any
+    # padding or quantisation: padding mismatched head dims to one width would
+    # make them pass.
+    if q.ndim != 3 or k.ndim != 3 or v.ndim != 3:
+        raise ValueError("expected flattened [tokens, heads, dim] tensors")
+    if k.shape != v.shape or q.shape[-1] != k.shape[-1]:
+        raise ValueError("K/V shapes and Q/K/V head dimensions must match")
     head_dim = q.shape[-1]
     run_dim = _padded_head_dim(head_dim)
-    if run_dim != head_dim and q.ndim == 3 and k.ndim == 3 and v.ndim == 3 and run_dim <= 128:
+    if run_dim != head_dim and run_dim <= 128:
         if sm_scale is None:
             sm_scale = head_dim ** -0.5
         out, mode = tilemix_attention_with_quant(
@@ -445,9 +473,9 @@ def tilemix_attention_with_quant(
 
 def _q_in_kernel_supported(block_m: int, BLKQ: int, mode_code: int, int8_use_fp16_v: bool) -> bool:
     """The kernel quantises Q per 128-row workgroup, which is one BLKQ = 128
-    block: block_m 128, and block_m 64 except with mixed routing on int8 V
-    codes (that variant runs 64-row workgroups)."""
-    wg128 = block_m == 128 or bool(int8_use_fp16_v) or mode_code != ROUTING_MODE_MIXED
+    block: block_m 128, 256 and 512, and block_m 64 except with mixed routing
+    on int8 V codes (that variant runs 64-row workgroups)."""
+    wg128 = block_m >= 128 or bool(int8_use_fp16_v) or mode_code != ROUTING_MODE_MIXED
     return wg128 and BLKQ == 128
 
 

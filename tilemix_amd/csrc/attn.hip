@@ -31,8 +31,8 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
     set_error("%s: head_dim must be a multiple of 16 in [16, 128], got %d", fn, p.head_dim);
     return TILEMIX_E_INVALID;
   }
-  if (p.block_m != 64 && p.block_m != 128) {
-    set_error("%s: block_m must be 64 or 128 in this build, got %d", fn, p.block_m);
+  if (p.block_m != 64 && p.block_m != 128 && p.block_m != 256 && p.block_m != 512) {
+    set_error("%s: block_m must be 64, 128, 256 or 512, got %d", fn, p.block_m);
     return TILEMIX_E_INVALID;
   }
   if (p.block_n != 64 && p.block_n != 128 && p.block_n != 256) {
@@ -60,7 +60,10 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   // fp16 or int8 routing the map is not read, with mixed routing each half of
   // the workgroup reads its own routing block.  Only mixed routing with int8 V
   // (which has no room for both K formats in LDS) keeps 64-row workgroups.
-  const int kind = p.block_m == 128 ? kAttn32
+  // block_m 256 / 512 run as 128-row workgroups too: the extra tiles a larger
+  // block visits are fully masked for a 128-row block's rows (an exact no-op),
+  // and each workgroup reads the routing row of the block that holds it.
+  const int kind = p.block_m >= 128 ? kAttn32
                  : p.routing_mode != TILEMIX_ROUTING_MIXED ? kAttn32
                  : int8v ? kAttn16 : kAttn32Split;
   const int wg_rows = kind == kAttn16 ? 64 : 128;
@@ -73,8 +76,8 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
     if (p.q_quant_in_kernel) {
       // The workgroup quantises its own 128 rows: one BLKQ = 128 block.
       if (wg_rows != 128 || p.blkq != 128) {
-        set_error("%s: q_quant_in_kernel needs BLKQ == 128 and 128-row workgroups (block_m 128, or block_m 64 "
-                  "without mixed int8-V routing); block_m=%d, BLKQ=%d", fn, p.block_m, p.blkq);
+        set_error("%s: q_quant_in_kernel needs BLKQ == 128 and 128-row workgroups (block_m 128, 256 or 512, or "
+                  "block_m 64 without mixed int8-V routing); block_m=%d, BLKQ=%d", fn, p.block_m, p.blkq);
         return TILEMIX_E_INVALID;
       }
     } else if (!p.q8 || !p.sq || !p.cu_q_scale) {
@@ -191,6 +194,7 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.group = p.heads_q / p.heads_k;
   a.d = p.head_dim;
   a.m_blocks = m_blocks;
+  a.route_shift = p.block_m == 512 ? 2 : p.block_m == 256 ? 1 : 0;
   a.mask_tiles = p.block_n_mask / kBN;
   a.ng = p.block_n / kBN;
   a.blkq = p.blkq > 0 ? p.blkq : 1;

@@ -37,6 +37,7 @@ struct AttnKArgs {
   float qk_scale;
   int hq, hk, group, d;
   int m_blocks;   // ceil(max_seqlen_q / rows per workgroup)
+  int route_shift; // log2(block_m / rows per workgroup) of the 128-row kernel: block_m 128 / 256 / 512
   int mask_tiles; // 64-key tiles per routing block: block_n_mask / 64
   int ng;         // 64-key tiles per online-softmax step: block_n / 64 (GEN kernels)
   int blkq, blkk;

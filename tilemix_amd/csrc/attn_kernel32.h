@@ -1,8 +1,9 @@
 // Fused FP16/INT8-routed flash-attention prefill forward for gfx950: the
 // 32-row kernel (4 waves x 32 query rows = 128 rows per workgroup).  It runs
-// block_m = 128 and, with SPLIT, block_m = 64: the workgroup's two 64-row
-// halves are two routing blocks, and a key tile whose route differs between
-// the halves is staged in both K formats.
+// block_m = 128; block_m = 256 and 512 as 128-row workgroups that read their
+// block's routing row; and, with SPLIT, block_m = 64: the workgroup's two
+// 64-row halves are two routing blocks, and a key tile whose route differs
+// between the halves is staged in both K formats.
 //
 // Numerics follow attn_fwd (attention/triton/tilemix.py:503-951):
 //   qk_scale = fp32(sm_scale) * fp32(log2 e)                               (:641)
@@ -131,9 +132,14 @@ attn32_kernel(const AttnKArgs a) {
   // of the high half; a high half past the sequence end takes the low half's).
   uint64_t bits = 0, bits_hi = 0;
   if (MODE == TILEMIX_ROUTING_MIXED) {
-    constexpr int RB = SPLIT ? BM / 2 : BM;  // rows per routing block
-    const int mbz = (Lq + RB - 1) / RB;      // per-sequence m_blocks (reference :819-820)
-    const int mb = SPLIT ? 2 * m : m;
+    // Rows per routing block: BM / 2 (SPLIT), else block_m = BM << route_shift.
+    // block_m 256 / 512 run as BM-row workgroups that share a routing row: a
+    // row's result depends only on its own route bits and causal range (the
+    // reference's extra tiles of a larger block are fully masked for it).
+    constexpr int LOG_BM = __builtin_ctz(BM);
+    const int rb_log = SPLIT ? LOG_BM - 1 : LOG_BM + a.route_shift;
+    const int mbz = (Lq + (1 << rb_log) - 1) >> rb_log;  // per-sequence m_blocks (reference :819-820)
+    const int mb = SPLIT ? 2 * m : m >> a.route_shift;
     bits = a.bitmask[hk * mbz + mb];
     if (SPLIT) bits_hi = mb + 1 < mbz ? a.bitmask[hk * mbz + mb + 1] : bits;
   }
@@ -377,7 +383,10 @@ attn32_kernel(const AttnKArgs a) {
     const int64_t qt_bytes = a.sq_t * 2;
     const unsigned char* qwave =
         reinterpret_cast<const unsigned char*>(a.q + (int64_t)(q_start + row0w) * a.sq_t + (int64_t)h * a.sq_h);
-    const SRsrc rs = make_srsrc(qwave, row0w < Lq ? (int)((Lq - row0w) * qt_bytes) : 0);
+    // Sized to the rows this wave reads (at most 32): the host keeps 128 * Q
+    // token stride below 2^31 bytes, so the size and every row offset stay
+    // below 2^31 and a padded-column lane's kOffOutside lies past the end.
+    const SRsrc rs = make_srsrc(qwave, row0w < Lq ? (int)(min(Lq - row0w, 32) * qt_bytes) : 0);
     const uint32_t qlds = smem_lds + STAGE + (uint32_t)(wave * 32 * ROW16);
 #pragma unroll
     for (int i = 0; i < QINS; ++i) {
