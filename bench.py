@@ -12,14 +12,16 @@ Printed: one JSON line.  ``value`` is effective TOPS of the whole step
 (algorithmic ops 4*B*Hq*D*L(L+1)/2 / step time); ``roofline`` refers to the
 attention kernel alone, timed with HIP events on the launch stream, against
 the blended fp16/int8 MFMA roofline of the routed tile mix; ``cpu_baseline``
-times the CPU oracle (numpy fp32 emulation) on a bounded slice of the same
-workload on this host; ``extra.e2e_prefill_ms`` is BASELINE configs[4] (random-
+times the PyTorch-eager fp32 emulation of the reference semantics
+(oracle/tilemix_torch_cpu.py) on a B = 1 slice of the same workload on this
+host, in TOPS and ms with the B = 8 time extrapolated x8 (labelled);
+``extra.e2e_prefill_ms`` is BASELINE configs[4] (random-
 init fp16 Llama-3.2-3B prefill, B=8 x 4096, TileMix SpTrans50 in every layer).
 
 The default run also reports, in ``extra``: the SpTrans p-sweep
 {0, .25, .5, .75, 1} (kernel and step), BASELINE configs 3 and 4 and the
 model glue's B8 x 2048 shapes (one step each), and BASELINE configs[0] (cfg1)
-on the GPU beside the CPU oracle's median of 20 runs.
+on the GPU beside the PyTorch-eager CPU emulation's median of 20 runs.
 
     python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu] [--no-e2e] [--no-sweep]
 """
@@ -287,60 +289,57 @@ def cfg1(device, runs: int = 20, warmup: int = 5, with_cpu: bool = True):
     gpu_ms = time_steps(fn, runs, warmup)
     out = {"gpu_step_ms": gpu_ms, "eff_tops": algorithmic_ops(1, hq, d, t) / (gpu_ms * 1e-3) / 1e12}
     if with_cpu:
-        qn = q.permute(0, 2, 1, 3).reshape(t, hq, d).numpy()
-        kn = k.permute(0, 2, 1, 3).reshape(t, hk, d).numpy()
-        vn = v.permute(0, 2, 1, 3).reshape(t, hk, d).numpy()
-        cu = np.array([0, t])
-        bits = np.array([int(x) for x in pmap.cpu().tolist()], dtype=np.uint64)
+        from oracle import tilemix_torch_cpu as T
+        qn = q.permute(0, 2, 1, 3).reshape(t, hq, d)
+        kn = k.permute(0, 2, 1, 3).reshape(t, hk, d)
+        vn = v.permute(0, 2, 1, 3).reshape(t, hk, d)
+        bits = [int(x) for x in pmap.cpu().tolist()]
 
-        def oracle():
-            q8, sq, cuq = O.quant_per_block_int8(qn, cu, 128)
-            k8, sk, cuk = O.quant_per_block_int8(kn, cu, 64)
-            return O.attn_fwd(qn, kn, vn, cu, cu, bits, block_m=64, block_n_mask=64, causal=True, q8=q8, k8=k8,
-                              sq16=sq.astype(np.float16), sk16=sk.astype(np.float16), cu_q_scale=cuq,
-                              cu_k_scale=cuk)
-        oracle()
+        def eager():
+            return T.attn_fwd_causal(qn, kn, vn, [0, t], bits, block_m=64, block_n_mask=64)
+        eager()
         times = []
         for _ in range(runs):
             t0 = time.perf_counter()
-            oracle()
+            eager()
             times.append((time.perf_counter() - t0) * 1e3)
-        out["cpu_oracle_median_ms"] = statistics.median(times)
-        out["cpu_note"] = f"median of {runs} runs after 1 warmup, numpy oracle on this host's CPU"
+        out["cpu_eager_median_ms"] = statistics.median(times)
+        out["cpu_note"] = (f"median of {runs} runs after 1 warmup, PyTorch-eager fp32 emulation "
+                           f"(oracle/tilemix_torch_cpu.py) on {torch.get_num_threads()} torch threads of this host")
     return out
 
 
-def cpu_baseline(q, k, v, bitmask_row, sample_groups: int = 4):
-    """Oracle (numpy fp32 emulation) on sequence 0, the first `sample_groups`
-    KV groups (3 query heads each), quantisation included; scaled to TOPS."""
-    import numpy as np
-    from threadpoolctl import threadpool_info
-    from oracle import tilemix_oracle as O
-    hq = sample_groups * (HQ // HK)
-    qs = q[:L, :hq].cpu().numpy()
-    ks = k[:L, :sample_groups].cpu().numpy()
-    vs = v[:L, :sample_groups].cpu().numpy()
-    cu = np.array([0, L])
-    bits = np.array([int(x) for x in bitmask_row.tolist()] * sample_groups, dtype=np.uint64)
-    t0 = time.perf_counter()
-    q8, sq, cuq = O.quant_per_block_int8(qs, cu, 128)
-    k8, sk, cuk = O.quant_per_block_int8(ks, cu, 64)
-    O.attn_fwd(qs, ks, vs, cu, cu, bits, block_m=128, block_n_mask=64, causal=True,
-               q8=q8, k8=k8, sq16=sq.astype(np.float16), sk16=sk.astype(np.float16),
-               cu_q_scale=cuq, cu_k_scale=cuk)
-    secs = time.perf_counter() - t0
-    ops = algorithmic_ops(b=1, hq=hq)
-    threads = max([i.get("num_threads", 1) for i in threadpool_info()] or [1])
+def cpu_baseline(q, k, v, bitmask_row, runs: int = 3):
+    """The PyTorch-eager CPU emulation of the reference semantics
+    (oracle/tilemix_torch_cpu.py: quantisation, both routes' scores, online
+    softmax per 64-key tile, fp16 V) on a B = 1 slice of the workload: sequence
+    0, all 24 query / 8 KV heads, 4096 tokens, SpTrans50.  Median of ``runs``
+    runs on this host's torch threads; reported as TOPS and as ms, with the
+    B = 8 time extrapolated x8 (sequences are independent work)."""
+    import torch
+    from oracle import tilemix_torch_cpu as T
+    qs, ks, vs = q[:L].cpu(), k[:L].cpu(), v[:L].cpu()
+    bits = [int(x) for x in bitmask_row.tolist()] * HK
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        T.attn_fwd_causal(qs, ks, vs, [0, L], bits, block_m=128, block_n_mask=64)
+        times.append(time.perf_counter() - t0)
+    secs = statistics.median(times)
+    ops = algorithmic_ops(b=1)
     host = host_cpu()
+    threads = torch.get_num_threads()
     return {
         "value": ops / secs / 1e12,
         "unit": "TOPS",
         "cores": int(threads),
         "kind": "port",
-        "sample": (f"numpy oracle (fp32 emulation incl. int8 quantisation), sequence 0, "
-                   f"{hq} query heads / {sample_groups} KV heads of the B8 L4096 SpTrans50 workload; "
-                   f"{secs:.2f} s for {ops:.3e} ops; BLAS threads {threads}; host {host['cpu_model']}, "
-                   f"os.cpu_count()={host['os_cpu_count']}, torch.get_num_threads()={host['torch_num_threads']}"),
+        "b1_ms": secs * 1e3,
+        "b8_ms_extrapolated_x8": secs * 1e3 * 8,
+        "sample": (f"PyTorch-eager fp32 emulation (int8 quantisation included) of sequence 0 of the B8 L4096 "
+                   f"SpTrans50 workload (all {HQ} query / {HK} KV heads): median of {runs} runs = "
+                   f"{secs * 1e3:.0f} ms for {ops:.3e} ops; B=8 extrapolated x8 = {secs * 8e3:.0f} ms; "
+                   f"{threads} torch threads on {host['cpu_model']} (os.cpu_count()={host['os_cpu_count']})"),
         "seconds": secs,
         **host,
     }
@@ -351,7 +350,7 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline (PyTorch-eager emulation)")
     ap.add_argument("--no-e2e", action="store_true", help="skip the e2e Llama-3.2-3B prefill timing")
     ap.add_argument("--no-sweep", action="store_true",
                     help="skip the SpTrans p-sweep, configs 1/3/4 and the glue shapes")

@@ -213,13 +213,21 @@ def test_cfg5_top1_agrees_with_oracle_attention(device, cfg5_model, monkeypatch)
           flush=True)
     agree, last, dmax, dmean = res["tilemix_vs_oracle"]
     c_agree, _, c_dmax, c_dmean = res["control_oracle_vs_oracle_fp32k16"]
-    # Oracle-stable positions: the two valid oracle models give the same top-1.
+    # Oracle-stable positions: the two valid oracle models give the same top-1
+    # and the exact oracle's top-2 gap is more than twice the largest logit
+    # difference between the two oracles at that position (a position inside
+    # that margin is a near-tie that any ulp-level difference can flip).
     t_got, t_ref, t_ref32 = got.argmax(-1), ref.argmax(-1), ref32.argmax(-1)
-    stable = t_ref == t_ref32
-    n_stable = int(stable.sum().item())
+    both = t_ref == t_ref32
+    gap_t = torch.from_numpy(gap).to(device).view(got.shape[:2])
+    dc = (ref32 - ref).abs().amax(-1)
+    stable = both & (gap_t > 2 * dc)
+    n_stable, n_both = int(stable.sum().item()), int(both.sum().item())
     agree_stable = (t_got == t_ref)[stable].float().mean().item()
-    print(f"cfg5 top-1 on oracle-stable positions: {agree_stable:.5f} over {n_stable} positions "
-          f"(all positions {agree:.5f})", flush=True)
+    agree_both = (t_got == t_ref)[both].float().mean().item()
+    print(f"cfg5 top-1 on oracle-stable positions: {agree_stable:.5f} over {n_stable} positions; "
+          f"where the two oracles agree: {agree_both:.5f} over {n_both}; all positions {agree:.5f} "
+          f"over {t_got.numel()}", flush=True)
     assert n_stable >= 2048, n_stable
     assert agree_stable >= 0.999, (agree_stable, n_stable)
     # Fixed floor on the all-position rate (measured 0.9873 over 2048 positions

@@ -49,6 +49,22 @@ def test_block_config_buckets(monkeypatch):
     assert a._get_block_config(256) == TL.BucketConfig(64, 64)
 
 
+@pytest.mark.parametrize("forced,want", [("256,64", (256, 64)), ("512,64", (512, 64))])
+def test_forced_fallback_block_m_is_rejected_by_the_model(monkeypatch, forced, want):
+    """Below every available block_n (40 tokens) the forced size falls back to
+    the nearest of block_m 64/128/256/512 (reference models/tilemix_llama.py:
+    137-140), and the model's forward then rejects a size outside
+    available_block_sizes with the reference's ValueError (:546-555); the
+    attention entry itself runs block_m 256 / 512 (GPU tests)."""
+    model = _tiny_llama(1)
+    TL.inject_tilemix_into_llama(model)
+    a = model.model.layers[0].self_attn
+    monkeypatch.setenv("TILEMIX_FORCE_CONFIG", forced)
+    assert (a._get_block_config(40).block_m, a._get_block_config(40).block_n) == want
+    with pytest.raises(ValueError, match="is not in available_block_sizes. This should not happen"):
+        a._routing_for(40, torch.device("cpu"))
+
+
 def test_inject_copies_weights_and_configure_clears_caches():
     model = _tiny_llama()
     before = {k: v.clone() for k, v in model.state_dict().items()}

@@ -264,7 +264,8 @@ class TileMixRoutingMixin:
         bnm = pick_mask_block_n(seqlen, cfg.block_n)
         if (cfg.block_m, cfg.block_n) not in self._block_to_candidate:
             raise ValueError(f"Block size {(cfg.block_m, cfg.block_n)} for bucket {self._choose_bucket(seqlen)} "
-                             f"is not in available_block_sizes. Available sizes: {self.available_block_sizes}")
+                             f"is not in available_block_sizes. This should not happen if _get_block_config is "
+                             f"working correctly. Available sizes: {self.available_block_sizes}")
         ptype, pparams = self._get_pattern_config(seqlen)
         full = self._prepare_precision_map(seqlen, cfg, bnm, ptype, pparams, device)
         expected = self.nkv * ((seqlen + cfg.block_m - 1) // cfg.block_m)
