@@ -1,0 +1,222 @@
+"""CPU checks of the generated assembly tile loop (tilemix_amd/csrc/attn_pipe_asm.h).
+
+* The committed header is exactly what gen_attn_pipe.py generates.
+* A static checker replays every straight-line compute body of the loop
+  (FILL / ITER for fp16 and int8 next tiles, DRAIN, both stage parities) and
+  enforces the gfx950 rules the generator relies on, since the compiler does
+  not look inside the asm statement:
+    - an LDS read has completed (s_waitcnt lgkmcnt accounting, in-order
+      return) before any instruction reads its destination;
+    - a VALU instruction reads an MFMA result no sooner than 18 wait states
+      after the MFMA (accumulation chains, MFMA -> the same MFMA's SrcC, excepted);
+    - an MFMA reads a VALU result no sooner than 3 wait states after it;
+    - no instruction reads the result of the v_exp_f32 right before it;
+    - v_permlane32_swap's operands were written at least 2 wait states earlier;
+    - a copy (buffer_load ... lds) is at least one wait state after the M0
+      write it uses.
+  Each rule is shown to catch a planted violation.
+* Structure: every body reads each K / V operand once per MFMA in the
+  reference's k-step order, and the row sum accumulates 16 pairs in order.
+"""
+from __future__ import annotations
+
+import re
+import sys
+from pathlib import Path
+
+import pytest
+
+REPO = Path(__file__).resolve().parent.parent
+CSRC = REPO / "tilemix_amd" / "csrc"
+sys.path.insert(0, str(CSRC))
+import gen_attn_pipe as G  # noqa: E402
+
+sys.path.pop(0)
+
+
+def test_committed_header_is_generated():
+    assert (CSRC / "attn_pipe_asm.h").read_text() == G.generate()
+
+
+_REG = re.compile(r"v\[(\d+):(\d+)\]|\bv(\d+)\b")
+
+
+def _regs(tok: str) -> set[int]:
+    out: set[int] = set()
+    for m in _REG.finditer(tok):
+        if m.group(1) is not None:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+        else:
+            out.add(int(m.group(3)))
+    return out
+
+
+def _parse(line: str):
+    op, _, rest = line.partition(" ")
+    args = [a.strip() for a in rest.split(",")] if rest else []
+    return op, args
+
+
+def _wait_states(op: str, args) -> int:
+    if op == "s_nop":
+        return int(args[0]) + 1
+    return 1
+
+
+def check_body(lines: list[str]) -> None:
+    """Raises AssertionError on the first violated rule."""
+    pending: list[set[int]] = []   # outstanding LDS reads, oldest first
+    inflight: set[int] = set()      # registers written by outstanding LDS reads
+    mfma_w: dict[int, tuple[int, int]] = {}  # reg -> (wait-state clock of the MFMA write, its dst base)
+    valu_w: dict[int, int] = {}     # reg -> clock of the last VALU write
+    clock = 0
+    prev_exp: set[int] = set()
+    for line in lines:
+        if line.endswith(":") or not line:
+            continue
+        op, args = _parse(line)
+        ws = _wait_states(op, args)
+        if op == "s_waitcnt":
+            m = re.match(r"lgkmcnt\((\d+)\)", args[0])
+            if m:
+                keep = int(m.group(1))
+                while len(pending) > keep:
+                    pending.pop(0)
+                inflight = set().union(*pending) if pending else set()
+            clock += ws
+            prev_exp = set()
+            continue
+        if op.startswith("s_") or op.startswith("buffer_"):
+            clock += ws
+            prev_exp = set()
+            continue
+        dst = _regs(args[0]) if args else set()
+        srcs = set().union(*(_regs(a) for a in args[1:])) if len(args) > 1 else set()
+        if op == "v_dot2c_f32_f16":
+            srcs |= dst
+        if op == "v_permlane32_swap_b32":
+            srcs |= dst
+        assert not (srcs & inflight), f"reads an LDS destination before its wait: {line}"
+        assert not (srcs & prev_exp), f"reads the exp result of the previous instruction: {line}"
+        if op.startswith("v_mfma"):
+            c_regs = _regs(args[3]) if len(args) > 3 else set()
+            for r in srcs:
+                if r in valu_w:
+                    assert clock - valu_w[r] >= 3, f"MFMA reads a VALU result too early: {line}"
+                if r in mfma_w and not (r in c_regs and r in dst):
+                    assert clock - mfma_w[r][0] >= 18, f"MFMA reads another MFMA's result too early: {line}"
+            for r in dst:
+                mfma_w[r] = (clock, min(dst))
+                valu_w.pop(r, None)
+        elif op.startswith("ds_read"):
+            assert not (dst & inflight), f"LDS destination reused before its wait: {line}"
+            pending.append(dst)
+            inflight |= dst
+        else:  # VALU
+            for r in srcs:
+                if r in mfma_w:
+                    assert clock - mfma_w[r][0] >= 18, f"VALU reads an MFMA result too early: {line}"
+                if op == "v_permlane32_swap_b32" and r in valu_w:
+                    assert clock - valu_w[r] >= 2, f"permlane operand written too late: {line}"
+            for r in dst:
+                valu_w[r] = clock
+                mfma_w.pop(r, None)
+        prev_exp = dst if op == "v_exp_f32" else set()
+        clock += ws
+
+
+def check_m0(lines: list[str]) -> None:
+    last_m0 = None
+    clock = 0
+    for line in lines:
+        if line.endswith(":"):
+            continue
+        op, args = _parse(line)
+        if op.startswith("s_") and args and args[0] == "m0":
+            last_m0 = clock
+        if op.startswith("buffer_load") and line.endswith("lds"):
+            assert last_m0 is not None and clock - last_m0 >= 2, f"copy right after its M0 write: {line}"
+        clock += _wait_states(op, args)
+
+
+def _bodies():
+    out = {}
+    for mixed_regs in (False, True):
+        for kind in ("f16", "i8"):
+            if kind == "i8" and not mixed_regs:
+                continue
+            for par in (0, 1):
+                out[f"iter_{kind}_p{par}_{mixed_regs}"] = G.body_iter(kind, 1 - par, par, mixed_regs, 1 - par)
+            out[f"fill_{kind}_{mixed_regs}"] = G.body_fill(kind, 0, mixed_regs)
+        for par in (0, 1):
+            out[f"drain_p{par}_{mixed_regs}"] = G.body_iter("none", 0, par, mixed_regs, 0)
+    return out
+
+
+BODIES = _bodies()
+
+
+@pytest.mark.parametrize("name", sorted(BODIES))
+def test_body_hazards(name):
+    check_body(BODIES[name])
+
+
+@pytest.mark.parametrize("mode", ["f16", "i8", "mixed"])
+def test_loop_m0_rule(mode):
+    check_m0(G.loop_asm(mode))
+
+
+def _planted(lines, pred, repl):
+    out = list(lines)
+    for i, ln in enumerate(out):
+        if pred(ln):
+            out[i:i + 1] = repl(ln)
+            return out
+    raise AssertionError("no line to plant in")
+
+
+@pytest.mark.parametrize("plant", ["drop_lds_wait", "early_conversion", "rescale_late", "exp_then_use",
+                                   "permlane_no_nop", "m0_no_nop"])
+def test_checker_catches_planted_violations(plant):
+    body = BODIES["iter_f16_p0_True"]
+    if plant == "drop_lds_wait":
+        bad = _planted(body, lambda ln: ln.startswith("s_waitcnt lgkmcnt(3)"), lambda ln: [])
+    elif plant == "early_conversion":
+        # read the first QK accumulator pair right after the last QK MFMA
+        idx = max(i for i, ln in enumerate(body) if ln.startswith("v_mfma_f32_32x32x16_f16 v[96:111]"))
+        bad = body[:idx + 1] + [f"v_cvt_pk_f16_f32 v{G.T}, v96, v97"] + body[idx + 1:]
+    elif plant == "rescale_late":
+        idx = next(i for i, ln in enumerate(body) if ln.startswith("v_mfma_f32_32x32x16_f16 v[16:31]"))
+        bad = body[:idx] + [f"v_mul_f32 v16, %[al], v16"] + body[idx:]
+    elif plant == "exp_then_use":
+        idx = next(i for i, ln in enumerate(body) if ln.startswith("v_exp_f32"))
+        r = _parse(body[idx])[1][0]
+        bad = body[:idx + 1] + [f"v_mov_b32 v{G.T + 5}, {r}"] + body[idx + 1:]
+    elif plant == "permlane_no_nop":
+        bad = _planted(body, lambda ln: ln == "s_nop 1", lambda ln: [])
+    else:
+        loop = G.loop_asm("mixed")
+        bad = _planted(loop, lambda ln: ln == "s_nop 0", lambda ln: [])
+        with pytest.raises(AssertionError):
+            check_m0(bad)
+        return
+    with pytest.raises(AssertionError):
+        check_body(bad)
+
+
+def test_bodies_read_operands_in_kstep_order():
+    body = BODIES["iter_f16_p0_True"]
+    qk = [ln for ln in body if ln.startswith("v_mfma_f32_32x32x16_f16 v[80:95]") or
+          ln.startswith("v_mfma_f32_32x32x16_f16 v[96:111]")]
+    assert [int(re.search(r"%\[qf(\d)\]", ln).group(1)) for ln in qk] == list(range(8)) * 2
+    assert qk[0].endswith(", 0") and qk[8].endswith(", 0")
+    pv = [ln for ln in body if re.match(r"v_mfma_f32_32x32x16_f16 v\[(0|16|32|48):", ln)]
+    assert len(pv) == 16
+    for db in range(4):
+        chain = [ln for ln in pv if ln.startswith(f"v_mfma_f32_32x32x16_f16 v[{16 * db}:")]
+        assert [re.search(r"v\[(\d+):\d+\], v\[\d+:\d+\]$", ln).group(1) for ln in chain] == \
+            [str(G.P + 4 * ks) for ks in range(4)]
+    dots = [ln for ln in body if ln.startswith("v_dot2c_f32_f16")]
+    assert [int(ln.split("v")[-1]) - G.P for ln in dots] == list(range(16))
+    i8 = [ln for ln in BODIES["iter_i8_p0_True"] if ln.startswith("v_mfma_i32_32x32x32_i8")]
+    assert [int(re.search(r"%\[q8f(\d)\]", ln).group(1)) for ln in i8] == list(range(4)) * 2

@@ -3,6 +3,7 @@
 #include "attn_common.h"
 
 #include <algorithm>
+#include <cstdlib>
 
 namespace tmx {
 
@@ -205,6 +206,12 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
   a.q_fused = (need_int8 && p.q_quant_in_kernel) ? 1 : 0;
   const bool dump = dump_i32 != nullptr || dump_f16 != nullptr;
   a.total_items = (int)total;
+  // The pipelined assembly tile body (head_dim 128, 128-row workgroups, fp16 V,
+  // no bias, block_n 64); TILEMIX_HIP_PIPE=0 selects the C++ tile body.
+  {
+    const char* env = getenv("TILEMIX_HIP_PIPE");
+    a.pipe = (env != nullptr && env[0] == '0') ? 0 : 1;
+  }
   a.per_xcd = (int)work_items_per_xcd((int64_t)p.heads_k * p.batch, (int64_t)m_blocks * a.group);
 
   const int dp = p.head_dim <= 64 ? 64 : 128;

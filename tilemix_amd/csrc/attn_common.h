@@ -45,6 +45,7 @@ struct AttnKArgs {
   int q_fused;      // Q quantised in the attention kernel (128-row workgroups, BLKQ == 128)
   int total_items;  // (sequence, query head, query block) work items
   int per_xcd;
+  int pipe;         // the pipelined assembly tile body may serve this launch
 };
 
 // Work item of workgroup `bid`, or -1.  Items are numbered

@@ -52,13 +52,16 @@
 #pragma once
 
 #include "attn_common.h"
+#include "attn_pipe_asm.h"
 
 namespace tmx {
 
-template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS, bool SPLIT, bool GEN>
+template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS, bool SPLIT, bool GEN, bool PIPE = false>
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn32_kernel(const AttnKArgs a) {
   static_assert(!SPLIT || (NW % 2 == 0 && !INT8V), "split workgroups: even wave count, fp16 V");
+  static_assert(!PIPE || (NW == 4 && DP == 128 && !INT8V && !DUMP && !BIAS && !SPLIT && !GEN),
+                "the pipelined tile body serves the plain 4-wave head_dim-128 launch");
   constexpr int BM = NW * 32;
   // K/V scales per tile and lane: one, or (GEN) one per 4-key group g = 4 kb + jj
   // of the lane's keys 32 kb + 8 jj + 4 hi .. + 3.
@@ -204,8 +207,8 @@ attn32_kernel(const AttnKArgs a) {
   int toff_k16 = 0, toff_k8 = 0, toff_v16 = 0, toff_v8 = 0;
   const int tstep_k16 = kBN * (int)kt_bytes, tstep_k8 = kBN * (int)k8t_bytes;
   const int tstep_v16 = kBN * (int)vt_bytes, tstep_v8 = kBN * (int)v8t_bytes;
-  // with_v = false (a GEN max pass) copies the K tile only.
-  auto issue_tile = [&](int route, uint32_t stage, bool with_v) {
+  // K part of a tile copy (the format(s) of the tile's route) into stage's K slot.
+  auto issue_k = [&](int route, uint32_t stage) {
     const bool need16 = MODE != TILEMIX_ROUTING_INT8 && (SPLIT ? route != 3 : route == 0);
     const bool need8 = MODE != TILEMIX_ROUTING_FP16 && route != 0;
     if (need16) {
@@ -227,9 +230,13 @@ attn32_kernel(const AttnKArgs a) {
       for (int i = 0; i < K8_INS; ++i)
         async_load16_asm(rs, o + i * step_k8, stage + K8OFF + (i * NW + wave) * 1024);
     }
+    toff_k16 += tstep_k16;
+    if (MODE != TILEMIX_ROUTING_FP16) toff_k8 += tstep_k8;
+  };
+  // V part of a tile copy into stage's V slot (int8 V codes: the free half of the K slot).
+  auto issue_v = [&](int route, uint32_t stage) {
     const uint32_t vstage = stage + KBUF;
-    if (!with_v) {
-    } else if (!INT8V || route == 0) {
+    if (!INT8V || route == 0) {
       const SRsrc rs = rs_v16;
       int o = dma_v16 + toff_v16;
       asm volatile("" : "+v"(o));
@@ -244,10 +251,13 @@ attn32_kernel(const AttnKArgs a) {
       for (int i = 0; i < V8_INS; ++i)
         async_load16_asm(rs, o + i * step_v8, stage + V8OFF + (i * NW + wave) * 1024);
     }
-    toff_k16 += tstep_k16;
     toff_v16 += tstep_v16;
-    if (MODE != TILEMIX_ROUTING_FP16) toff_k8 += tstep_k8;
     if (INT8V) toff_v8 += tstep_v8;
+  };
+  // with_v = false (a GEN max pass) copies the K tile only.
+  auto issue_tile = [&](int route, uint32_t stage, bool with_v) {
+    issue_k(route, stage);
+    if (with_v) issue_v(route, stage);
   };
 
   // int8 V codes -> fp16 V tile (the layout of an fp16 V copy).  Each wave
@@ -307,9 +317,12 @@ attn32_kernel(const AttnKArgs a) {
   };
   // Issues the next tile (index nx) and fetches its scales; the loads land
   // before the barrier that precedes the tile's compute.
-  auto issue_next = [&](int nx, uint32_t stage, int& route, f16 (&skv)[NSG], f16 (&svv)[NSG]) {
+  // The K part (with the K scale and the route/scale bookkeeping) and the V
+  // part can go out at different times (the pipelined loop copies K a tile
+  // ahead of V); issue_next issues both.
+  auto issue_next_k = [&](int nx, uint32_t stage, int& route, f16 (&skv)[NSG], f16 (&svv)[NSG]) {
     route = tile_route(nx, nx_grp);
-    issue_tile(route, stage, true);
+    issue_k(route, stage);
     if (MODE != TILEMIX_ROUTING_FP16 && route != 0) {
       skv[0] = has_ks ? *skp : (f16)1.0f;
       if (INT8V) svv[0] = has_vs ? *svp : (f16)1.0f;
@@ -323,6 +336,10 @@ attn32_kernel(const AttnKArgs a) {
       if (MODE != TILEMIX_ROUTING_FP16 && skp != sk_last) skp += a.hk;
       if (INT8V && svp != sv_last) svp += a.hk;
     }
+  };
+  auto issue_next = [&](int nx, uint32_t stage, int& route, f16 (&skv)[NSG], f16 (&svv)[NSG]) {
+    issue_next_k(nx, stage, route, skv, svv);
+    issue_v(route, stage);
   };
 
   // ---- GEN: steps over (tile, pass) ---------------------------------------
@@ -768,8 +785,142 @@ attn32_kernel(const AttnKArgs a) {
     }
   };
 
+  // ---- software-pipelined loop (PIPE) -------------------------------------
+  // Tiles [0, n_sw) need no mask for any row of the workgroup (every key below
+  // Lk and, causal, at or below the first row's diagonal).  They run through
+  // the assembly tile body of attn_pipe_asm.h: iteration n computes tile n's
+  // softmax and PV beside tile n+1's QK, conversion and row maximum.  K is
+  // copied a tile ahead of V: iteration n issues K(n+2) into tile n's K slot
+  // and V(n+1) into tile n-1's V slot, both free after the iteration's
+  // barrier.  The remaining tiles (the causal diagonal, a ragged end) continue
+  // through the C++ body below, with K(n_sw) and V(n_sw) already in flight.
+  int n_sw = 0;
+  if constexpr (PIPE) {
+    int nf = Lk / kBN;
+    if (a.causal) {
+      const int lim = m * BM + diag + 1;  // keys below lim are valid for every row of the workgroup
+      nf = min(nf, lim <= 0 ? 0 : lim / kBN);
+    }
+    n_sw = max(0, min(nf, n_blocks));
+  }
+  if constexpr (PIPE) {
+    if (n_sw > 0) {
+      PipeState st;
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) st.acc[db] = acc[db];
+      st.s16 = (u32x16){};
+      st.mn = m_i;
+      st.al = 1.0f;
+      st.ng = 0.0f;
+      st.li = l_i;
+      PipeOps po;
+      const int kb16 = l32 * ROW16 + ((16 * hi) ^ (16 * swz_k<ROW16>(l32)));
+      const int kb8 = l32 * ROW8 + ((16 * hi) ^ (16 * swz_k<ROW8>(l32)));
+      const int j16 = lane & 15, g16 = (lane >> 4) & 1, vrl = 4 * hi + (j16 >> 2);
+      const int vb = vrl * ROW16 +
+                     (((16 * (2 * g16 + ((j16 & 3) >> 1))) ^ (16 * swz_v32<ROW16>(vrl))) | (8 * (j16 & 1)));
+#pragma unroll
+      for (int ks = 0; ks < 8; ++ks) po.ka[ks] = (int)smem_lds + (kb16 ^ (32 * ks));
+#pragma unroll
+      for (int ks = 0; ks < 4; ++ks) po.k8a[ks] = (int)smem_lds + K8OFF + (kb8 ^ (32 * ks));
+#pragma unroll
+      for (int db = 0; db < 4; ++db) po.va[db] = (int)smem_lds + (vb ^ (64 * db));
+      if constexpr (MODE != TILEMIX_ROUTING_INT8) {
+#pragma unroll
+        for (int ks = 0; ks < 8; ++ks) po.qf[ks] = qf[ks];
+      }
+      if constexpr (MODE != TILEMIX_ROUTING_FP16) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ++ks) po.q8f[ks] = q8f[ks];
+      }
+      po.fmax = 3.40282347e38f;
+
+      PipeCopy c;
+      c.tok16 = toff_k16;
+      c.tok8 = toff_k8;
+      c.tov16 = toff_v16;
+      c.grp = nx_grp;
+      c.gc = nx_gc;
+      c.sc = nx_sc;
+      c.rn = route_next;
+      c.sk[0] = __builtin_bit_cast(uint16_t, sk_next[0]);
+      c.sk[1] = 0;
+      c.nsw = n_sw;
+      c.nblk = n_blocks;
+      c.act = row0w < Lq ? 1 : 0;
+      c.bits = bits;
+      c.mt = a.mask_tiles;
+      c.kbt = kb_tiles;
+      c.hask = has_ks ? 1 : 0;
+      c.hk2 = a.hk * 2;
+      c.rsk16 = rs_k16.w;
+      c.rsk8 = rs_k8.w;
+      c.rsv16 = rs_v16.w;
+      c.stpk16 = step_k16;
+      c.stpk8 = step_k8;
+      c.stpv16 = step_v16;
+      c.tsk16 = tstep_k16;
+      c.tsk8 = tstep_k8;
+      c.tsv16 = tstep_v16;
+      c.ldsw = (int)smem_lds + wave * 1024;
+      c.dk16 = dma_k16;
+      c.dk8 = dma_k8;
+      c.dv16 = dma_v16;
+      c.sq16 = __builtin_bit_cast(uint16_t, sq16);
+      c.qks = a.qk_scale;
+      c.magic2 = 0x4B4000004B400000ull;
+      if constexpr (MODE != TILEMIX_ROUTING_FP16) {
+        // K scales through a raw buffer over the whole array (every lookup is
+        // clamped to the sequence's blocks); offsets in bytes.
+        const SRsrc rs = make_srsrc(a.sk, 0x7fffffff);
+        c.rssk = rs.w;
+        c.skoff = has_ks ? (int)((skp - a.sk) * 2) : 0;
+        c.sklast = has_ks ? (int)((sk_last - a.sk) * 2) : 0;
+      } else {
+        c.rssk = (i32x4){};
+        c.skoff = c.sklast = 0;
+      }
+      // Every SGPR operand as a wave-uniform value (they are; readfirstlane
+      // tells the compiler).
+      {
+        auto u = [](int x) { return __builtin_amdgcn_readfirstlane(x); };
+        auto u64 = [&](uint64_t x) {
+          return (uint64_t)(uint32_t)u((int)(uint32_t)x) | ((uint64_t)(uint32_t)u((int)(x >> 32)) << 32);
+        };
+        auto u4 = [&](i32x4 x) { return (i32x4){u(x[0]), u(x[1]), u(x[2]), u(x[3])}; };
+        c.tok16 = u(c.tok16); c.tok8 = u(c.tok8); c.tov16 = u(c.tov16);
+        c.grp = u(c.grp); c.gc = u(c.gc); c.sc = u(c.sc); c.skoff = u(c.skoff); c.rn = u(c.rn);
+        c.nsw = u(c.nsw); c.nblk = u(c.nblk); c.act = u(c.act); c.bits = u64(c.bits);
+        c.mt = u(c.mt); c.kbt = u(c.kbt); c.hask = u(c.hask); c.sklast = u(c.sklast); c.hk2 = u(c.hk2);
+        c.rssk = u4(c.rssk); c.rsk16 = u4(c.rsk16); c.rsk8 = u4(c.rsk8); c.rsv16 = u4(c.rsv16);
+        c.stpk16 = u(c.stpk16); c.stpk8 = u(c.stpk8); c.stpv16 = u(c.stpv16);
+        c.tsk16 = u(c.tsk16); c.tsk8 = u(c.tsk8); c.tsv16 = u(c.tsv16); c.ldsw = u(c.ldsw);
+        c.qks = __int_as_float(u(__float_as_int(c.qks)));
+      }
+      if constexpr (MODE == TILEMIX_ROUTING_FP16) pipe_loop_f16(st, po, c);
+      else if constexpr (MODE == TILEMIX_ROUTING_INT8) pipe_loop_i8(st, po, c);
+      else pipe_loop_mixed(st, po, c);
+
+#pragma unroll
+      for (int db = 0; db < NDB; ++db) acc[db] = st.acc[db];
+      m_i = st.mn;
+      l_i = st.li;
+      toff_k16 = c.tok16;
+      toff_k8 = c.tok8;
+      toff_v16 = c.tov16;
+      nx_grp = c.grp;
+      nx_gc = c.gc;
+      nx_sc = c.sc;
+      route_next = c.rn;
+      sk_next[0] = __builtin_bit_cast(f16, (uint16_t)((n_sw & 1) ? c.sk[1] : c.sk[0]));
+      if constexpr (MODE != TILEMIX_ROUTING_FP16) {
+        if (has_ks) skp = a.sk + c.skoff / 2;
+      }
+    }
+  }
+
   if constexpr (!GEN) {
-    for (int n = 0; n < n_wave; ++n) {
+    for (int n = n_sw; n < n_wave; ++n) {
       const int route = SPLIT ? (route_next >> half) & 1 : route_next;
       const f16 skc[NSG] = {sk_next[0]};
       const f16 svc[NSG] = {sv_next[0]};
@@ -789,7 +940,7 @@ attn32_kernel(const AttnKArgs a) {
       const float alpha = has ? fast_exp2(m_i - m_next) : 1.0f;
       tile_update(stage, route, svc, s16, m_next, alpha);
     }
-    for (int n = n_wave; n < n_blocks; ++n) tile_start(n);
+    for (int n = max(n_wave, n_sw); n < n_blocks; ++n) tile_start(n);
   } else {
     // Steps of tiles n >= n_wave are no-ops for this wave (fully masked rows)
     // in both passes: the wave keeps the barriers and copies going only.

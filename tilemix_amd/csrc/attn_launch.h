@@ -24,6 +24,13 @@ struct AttnLauncher {
         return;
       }
     }
+    if constexpr (DP == 128 && !INT8V && !DUMP && !BIAS && !GEN) {
+      if (a.pipe) {
+        hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, false, GEN, true>), grid, block, 0, stream,
+                           a);
+        return;
+      }
+    }
     hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, false, GEN>), grid, block, 0, stream, a);
   }
 

@@ -69,6 +69,13 @@ def sources() -> list[Path]:
 def build(verbose: bool = False, jobs: int | None = None) -> Path:
     """Compile every HIP source for gfx950 and link the shared library."""
     hipcc = _hipcc()
+    # The pipelined tile loop's assembly is generated (attn_pipe_asm.h).
+    sys.path.insert(0, str(CSRC))
+    try:
+        import gen_attn_pipe
+    finally:
+        sys.path.pop(0)
+    gen_attn_pipe.write()
     BUILD_DIR.mkdir(parents=True, exist_ok=True)
     srcs = sources()
     objs = [BUILD_DIR / (s.stem + ".o") for s in srcs]
