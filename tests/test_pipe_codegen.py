@@ -204,6 +204,49 @@ def test_checker_catches_planted_violations(plant):
         check_body(bad)
 
 
+OPTION_SETS = [{}, {"copy_at": 1}, {"skip_refill": True}, {"skip_rescale": True}, {"qk_il": True},
+               {"pv_il": True}, {"copy_at": 3, "skip_refill": True, "skip_rescale": True, "qk_il": True,
+                                 "pv_il": True}]
+
+
+@pytest.fixture
+def opts():
+    saved = dict(G.OPTS)
+    yield G.OPTS
+    G.OPTS.clear()
+    G.OPTS.update(saved)
+
+
+@pytest.mark.parametrize("option_set", OPTION_SETS, ids=lambda o: "-".join(sorted(o)) or "default")
+def test_every_schedule_option_keeps_the_work(opts, option_set):
+    """Under every schedule option each body still passes the hazard rules,
+    rescales every O register exactly once (ITER / DRAIN), writes every score
+    register exactly once (FILL / ITER), packs every p register once and
+    accumulates the 16 pairs of the row sum."""
+    opts.update(option_set)
+    for name, body in _bodies().items():
+        check_body(body)
+        muls = [ln for ln in body if ln.startswith("v_mul_f32 v") and "%[al]" in ln]
+        targets = sorted(int(ln.split()[1].rstrip(",")[1:]) for ln in muls)
+        conv = [ln for ln in body if ln.startswith("v_cvt_pk_f16_f32 v") and
+                G.S16 <= int(ln.split()[1].rstrip(",")[1:]) < G.S16 + 16]
+        packs = [ln for ln in body if ln.startswith("v_cvt_pk_f16_f32 v") and
+                 G.P <= int(ln.split()[1].rstrip(",")[1:]) < G.P + 16]
+        dots = [ln for ln in body if ln.startswith("v_dot2c_f32_f16")]
+        if name.startswith("fill"):
+            assert not muls and not packs and not dots, name
+            assert sorted(int(ln.split()[1].rstrip(",")[1:]) for ln in conv) == list(range(G.S16, G.S16 + 16))
+        else:
+            assert targets == list(range(64)), (name, len(targets))
+            assert sorted(int(ln.split()[1].rstrip(",")[1:]) for ln in packs) == list(range(G.P, G.P + 16))
+            assert len(dots) == 16
+            if not name.startswith("drain"):
+                assert sorted(int(ln.split()[1].rstrip(",")[1:]) for ln in conv) == \
+                    list(range(G.S16, G.S16 + 16)), name
+    for mode in ("f16", "i8", "mixed"):
+        check_m0(G.loop_asm(mode))
+
+
 def test_bodies_read_operands_in_kstep_order():
     body = BODIES["iter_f16_p0_True"]
     qk = [ln for ln in body if ln.startswith("v_mfma_f32_32x32x16_f16 v[80:95]") or

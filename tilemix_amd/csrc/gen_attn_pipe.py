@@ -84,6 +84,32 @@ ROW16, ROW8 = 256, 128
 NW = 4
 K16_INS, K8_INS, V16_INS = 4, 2, 4  # 1 KB copies per wave and tile
 
+# Schedule options (the defaults are the measured production choice):
+#   copy_at       the tile copies go out after this phase-A MFMA (None: before
+#                 the compute body);
+#   skip_refill   the INT8 accumulator refill is skipped when the tile after
+#                 next is an FP16 tile;
+#   skip_rescale  the O rescale is skipped when alpha = 1 on every row of the
+#                 wave (an exact no-op then).
+#   qk_il         the two QK chains (kb 0, kb 1) alternate MFMA by MFMA;
+#   pv_il         the PV chains of d blocks (0, 1) and then (2, 3) alternate.
+OPTS = {"copy_at": None, "skip_refill": False, "skip_rescale": False, "qk_il": False, "pv_il": False}
+
+
+def qk_step(i: int, nm: int) -> tuple[int, int]:
+    """(kb, ks) of the i-th QK MFMA of a tile with nm MFMAs (k-steps in order per chain)."""
+    if OPTS["qk_il"]:
+        return i % 2, i // 2
+    return divmod(i, nm // 2)
+
+
+def pv_step(i: int) -> tuple[int, int]:
+    """(db, ks) of the i-th PV MFMA (k-steps in order per d block)."""
+    if OPTS["pv_il"]:
+        half, r = divmod(i, 8)
+        return 2 * half + r % 2, r // 2
+    return divmod(i, 4)
+
 
 def vr(a: int, n: int) -> str:
     return f"v[{a}:{a + n - 1}]" if n > 1 else f"v{a}"
@@ -96,17 +122,17 @@ def slot(i: int) -> str:
 # ---- compute blocks -----------------------------------------------------------
 
 def read_k16(i: int, kslot: int) -> str:
-    kb, ks = divmod(i, 8)
+    kb, ks = qk_step(i, 16)
     return f"ds_read_b128 {slot(i)}, %[ka{ks}] offset:{kslot * STAGE + kb * 32 * ROW16}"
 
 
 def read_k8(i: int, kslot: int) -> str:
-    kb, ks = divmod(i, 4)
+    kb, ks = qk_step(i, 8)
     return f"ds_read_b128 {slot(i)}, %[k8a{ks}] offset:{kslot * STAGE + kb * 32 * ROW8}"
 
 
 def mfma_k16(i: int) -> str:
-    kb, ks = divmod(i, 8)
+    kb, ks = qk_step(i, 16)
     d = QA if kb == 0 else QB
     c = "0" if ks == 0 else vr(d, 16)
     return f"v_mfma_f32_32x32x16_f16 {vr(d, 16)}, {slot(i)}, %[qf{ks}], {c}"
@@ -115,20 +141,20 @@ def mfma_k16(i: int) -> str:
 def mfma_k8(i: int) -> str:
     # The first k-step accumulates on top of the magic bias preloaded in the
     # accumulator registers.
-    kb, ks = divmod(i, 4)
+    kb, ks = qk_step(i, 8)
     d = QA if kb == 0 else QB
     return f"v_mfma_i32_32x32x32_i8 {vr(d, 16)}, {slot(i)}, %[q8f{ks}], {vr(d, 16)}"
 
 
 def reads_v(i: int, vslot: int) -> list[str]:
-    db, ks = divmod(i, 4)
+    db, ks = pv_step(i)
     base = RING + 4 * (i % 4)
     return [f"ds_read_b64_tr_b16 {vr(base + 2 * h2, 2)}, %[va{db}] "
             f"offset:{vslot * STAGE + VOFF + (16 * ks + 8 * h2) * ROW16}" for h2 in range(2)]
 
 
 def mfma_pv(i: int) -> str:
-    db, ks = divmod(i, 4)
+    db, ks = pv_step(i)
     a = vr(ACC[db], 16)
     return f"v_mfma_f32_32x32x16_f16 {a}, {slot(i)}, {vr(P + 4 * ks, 4)}, {a}"
 
@@ -234,21 +260,28 @@ def spread(items: list[str], n: int) -> list[list[str]]:
     return out
 
 
-def phase_a(kind: str, kslot: int, valu: list[str]) -> list[str]:
-    """kind: 'f16' / 'i8' QK of the next tile, or 'none' (VALU only)."""
+def phase_a(kind: str, kslot: int, valu: list[str], copy: list[str] | None = None,
+            tail: list[str] | None = None) -> list[str]:
+    """kind: 'f16' / 'i8' QK of the next tile, or 'none' (VALU only).  copy:
+    the tile copies, placed after MFMA OPTS['copy_at']; tail: after the last
+    chunk."""
+    copy, tail = copy or [], tail or []
     if kind == "none":
-        return list(valu)
+        return copy + list(valu) + tail
     nm = 16 if kind == "f16" else 8
     rd = read_k16 if kind == "f16" else read_k8
     mf = mfma_k16 if kind == "f16" else mfma_k8
     out = [rd(i, kslot) for i in range(4)]
     chunks = spread(valu, nm)
+    at = min(OPTS["copy_at"] or 0, nm - 1)
     for i in range(nm):
         out += [f"s_waitcnt lgkmcnt({min(3, nm - 1 - i)})", mf(i)]
         if i + 4 < nm:
             out.append(rd(i + 4, kslot))
+        if i == at:
+            out += copy
         out += chunks[i]
-    return out
+    return out + tail
 
 
 def phase_b(vslot: int, chunks: list[list[str]], tail: list[str]) -> list[str]:
@@ -263,46 +296,80 @@ def phase_b(vslot: int, chunks: list[list[str]], tail: list[str]) -> list[str]:
     return out + tail
 
 
-def b_chunks(kind: str, mixed_regs: bool) -> tuple[list[list[str]], list[str]]:
+def guard_rescale(lines: list[str], lbl: str) -> list[str]:
+    """Skip an O rescale block when no lane has alpha != 1 (VCC, set at the
+    start of the body)."""
+    return [f"s_cbranch_vccz {lbl}"] + lines + [f"{lbl}:"]
+
+
+def guard_refill(lines: list[str], lbl: str) -> list[str]:
+    """Skip an accumulator refill when the tile after next is an FP16 tile."""
+    return ["s_cmp_eq_u32 %[rn2], 0", f"s_cbranch_scc1 {lbl}"] + lines + [f"{lbl}:"]
+
+
+def b_chunks(kind: str, mixed_regs: bool, lbl: str) -> tuple[list[list[str]], list[str]]:
     """VALU of phase B: the l update and the O rescale of d blocks 1..3 (each
     done a chunk before the first MFMA into that block), and, with a next
     tile, its conversion, the accumulator refill and the row maximum."""
     r1, r2, r3 = rescale(1), rescale(2), rescale(3)
     ch: list[list[str]] = [[] for _ in range(16)]
-    ch[0] = l_update() + r1[:5]
-    ch[1], ch[2] = r1[5:11], r1[11:]
-    ch[4], ch[5], ch[6] = r2[:5], r2[5:11], r2[11:]
-    ch[8], ch[9], ch[10] = r3[:5], r3[5:11], r3[11:]
+    if OPTS["pv_il"]:
+        # d blocks 0 and 1 are rescaled in phase A; 2 and 3 before MFMA 8
+        r23 = r2 + r3
+        ch[0] = l_update() + r23[:6]
+        for c in range(1, 6):
+            ch[c] = r23[6 * c:6 * c + 6]
+    elif OPTS["skip_rescale"]:
+        ch[0] = l_update() + guard_rescale(r1, f"{lbl}_rs1")
+        ch[4] = guard_rescale(r2, f"{lbl}_rs2")
+        ch[8] = guard_rescale(r3, f"{lbl}_rs3")
+    else:
+        ch[0] = l_update() + r1[:5]
+        ch[1], ch[2] = r1[5:11], r1[11:]
+        ch[4], ch[5], ch[6] = r2[:5], r2[5:11], r2[11:]
+        ch[8], ch[9], ch[10] = r3[:5], r3[5:11], r3[11:]
     tail: list[str] = []
     if kind != "none":
         i8 = kind == "i8"
-        ch[3] = conv(range(0, 4), i8)
-        ch[7] = conv(range(4, 8), i8) + MAX_A
-        ch[11] = conv(range(8, 12), i8) + MAX_B
-        ch[12] = conv(range(12, 16), i8) + MAX_C
-        ch[13] = MAX_D
-        ch[14] = MAX_E
-        ch[15] = MAX_F
+        ch[3] += conv(range(0, 4), i8)
+        ch[7] += conv(range(4, 8), i8) + MAX_A
+        ch[11] += conv(range(8, 12), i8) + MAX_B
+        ch[12] += conv(range(12, 16), i8) + MAX_C
+        ch[13] += MAX_D
+        ch[14] += MAX_E
+        ch[15] += MAX_F
         tail = list(MAX_TAIL)
         if mixed_regs:
             fa, fb = refill(QA), refill(QB)
-            ch[8] = ch[8] + fa[:4]
-            ch[9] = ch[9] + fa[4:]
-            ch[13] = ch[13] + fb[:4]
-            ch[14] = ch[14] + fb[4:]
+            if OPTS["skip_refill"]:
+                ch[9] = ch[9] + guard_refill(fa, f"{lbl}_rfa")
+                ch[14] = ch[14] + guard_refill(fb, f"{lbl}_rfb")
+            else:
+                ch[8] = ch[8] + fa[:4]
+                ch[9] = ch[9] + fa[4:]
+                ch[13] = ch[13] + fb[:4]
+                ch[14] = ch[14] + fb[4:]
     return ch, tail
 
 
-def body_iter(kind: str, kslot: int, vslot: int, mixed_regs: bool, par_next: int) -> list[str]:
+def body_iter(kind: str, kslot: int, vslot: int, mixed_regs: bool, par_next: int, lbl: str = ".Lb",
+              copy: list[str] | None = None) -> list[str]:
     out = ["s_waitcnt lgkmcnt(0)"]
+    if OPTS["skip_rescale"]:
+        out.append("v_cmp_neq_f32 vcc, 1.0, %[al]")
     if kind == "i8":
         out += int8_scale(par_next)
-    out += phase_a(kind, kslot, softmax_steps() + rescale(0))
-    ch, tail = b_chunks(kind, mixed_regs)
+    if OPTS["pv_il"]:
+        out += phase_a(kind, kslot, softmax_steps() + rescale(0) + rescale(1), copy)
+    elif OPTS["skip_rescale"]:
+        out += phase_a(kind, kslot, softmax_steps(), copy, guard_rescale(rescale(0), f"{lbl}_rs0"))
+    else:
+        out += phase_a(kind, kslot, softmax_steps() + rescale(0), copy)
+    ch, tail = b_chunks(kind, mixed_regs, lbl)
     return out + phase_b(vslot, ch, tail)
 
 
-def body_fill(kind: str, kslot: int, mixed_regs: bool) -> list[str]:
+def body_fill(kind: str, kslot: int, mixed_regs: bool, lbl: str = ".Lf") -> list[str]:
     out = ["s_waitcnt lgkmcnt(0)"]
     if kind == "i8":
         # tile 0's INT8 chains start from the magic bias as well
@@ -312,7 +379,10 @@ def body_fill(kind: str, kslot: int, mixed_regs: bool) -> list[str]:
     out += ["s_nop 15", "s_nop 3"]
     out += conv(range(16), kind == "i8")
     if mixed_regs:
-        out += refill(QA) + refill(QB)
+        if OPTS["skip_refill"]:
+            out += guard_refill(refill(QA) + refill(QB), f"{lbl}_rf")
+        else:
+            out += refill(QA) + refill(QB)
     out += MAX_A + MAX_B + MAX_C + MAX_D + MAX_E + MAX_F + MAX_TAIL
     return out
 
@@ -389,24 +459,36 @@ def copy_v(par: int) -> list[str]:
     return o + ["s_add_u32 %[tov16], %[tov16], %[tsv16]"]
 
 
+def copies(mode: str, par: int, lbl: str) -> list[str]:
+    """Iteration n's copies: K(n+2) while n + 2 <= n_sw and n + 2 < n_blocks
+    (its route -> %[rn2]), V(n+1) while n + 1 < n_blocks."""
+    out = ["s_add_u32 %[t], %[n], 2", "s_cmp_gt_u32 %[t], %[nsw]", f"s_cbranch_scc1 {lbl}_nok",
+           "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nok"]
+    out += copy_k(mode, par, f"{lbl}_ck")
+    out += ["s_mov_b32 %[rn2], %[r2]", f"{lbl}_nok:"]
+    out += ["s_add_u32 %[t], %[n], 1", "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nov"]
+    out += copy_v(par)
+    return out + [f"{lbl}_nov:"]
+
+
 def iteration(mode: str, par: int, lbl: str) -> list[str]:
     """Iteration n (n & 1 == par; %[n] holds n)."""
     mixed_regs = mode != "f16"
+    inner = OPTS["copy_at"] is not None
     out = ["s_waitcnt vmcnt(0)", "s_barrier", "s_mov_b32 %[rn2], %[rn]"]
-    # K(n+2) while n + 2 <= n_sw and n + 2 < n_blocks
-    out += ["s_add_u32 %[t], %[n], 2", "s_cmp_gt_u32 %[t], %[nsw]", f"s_cbranch_scc1 {lbl}_nok",
-            "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nok"]
-    out += copy_k(mode, par, f"{lbl}_ck")
-    out += ["s_mov_b32 %[rn2], %[r2]", f"{lbl}_nok:"]
-    # V(n+1) while n + 1 < n_blocks
-    out += ["s_add_u32 %[t], %[n], 1", "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nov"]
-    out += copy_v(par)
-    out += [f"{lbl}_nov:"]
+    if not inner:
+        out += copies(mode, par, f"{lbl}_c")
     # compute (waves whose rows all lie past the sequence end only copy)
-    out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {lbl}_end",
+    out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {lbl}_inact",
             "s_add_u32 %[t], %[n], 1", "s_cmp_ge_u32 %[t], %[nsw]", f"s_cbranch_scc1 {lbl}_drain"]
-    f16_body = body_iter("f16", 1 - par, par, mixed_regs, 1 - par)
-    i8_body = body_iter("i8", 1 - par, par, mixed_regs, 1 - par)
+
+    def cp(tag: str) -> list[str] | None:
+        return copies(mode, par, f"{lbl}_{tag}c") if inner else None
+
+    if mode in ("f16", "mixed"):
+        f16_body = body_iter("f16", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_f", cp("f"))
+    if mode in ("i8", "mixed"):
+        i8_body = body_iter("i8", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_i", cp("i"))
     if mode == "f16":
         out += f16_body
     elif mode == "i8":
@@ -417,7 +499,10 @@ def iteration(mode: str, par: int, lbl: str) -> list[str]:
         out += [f"s_branch {lbl}_end", f"{lbl}_i8:"]
         out += i8_body
     out += [f"s_branch {lbl}_end", f"{lbl}_drain:"]
-    out += body_iter("none", 0, par, mixed_regs, 0)
+    out += body_iter("none", 0, par, mixed_regs, 0, f"{lbl}_d", cp("d"))
+    out += [f"s_branch {lbl}_end", f"{lbl}_inact:"]
+    if inner:
+        out += copies(mode, par, f"{lbl}_xc")
     out += [f"{lbl}_end:", "s_mov_b32 %[rn], %[rn2]"]
     return out
 
@@ -432,8 +517,8 @@ def fill(mode: str, lbl: str) -> list[str]:
     out += copy_k(mode, 1, f"{lbl}_ck")
     out += ["s_mov_b32 %[rn2], %[r2]", f"{lbl}_nok:"]
     out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {lbl}_end"]
-    f16_body = body_fill("f16", 0, mixed_regs)
-    i8_body = body_fill("i8", 0, mixed_regs)
+    f16_body = body_fill("f16", 0, mixed_regs, f"{lbl}_bf")
+    i8_body = body_fill("i8", 0, mixed_regs, f"{lbl}_bi")
     if mode == "f16":
         out += f16_body
     elif mode == "i8":
@@ -500,7 +585,7 @@ def function(mode: str) -> str:
 {text}
       : {", ".join(outs)}
       : {", ".join(ins)}
-      : {clob}, "scc", "memory");
+      : {clob}, "vcc", "scc", "memory");
 }}
 '''
 
