@@ -62,7 +62,7 @@ struct AttnKArgs {
 __host__ __device__ inline int64_t work_items_per_xcd(int64_t groups, int64_t ipg) {
   return (groups / 8) * ipg + ((groups % 8) * ipg + 7) / 8;
 }
-__device__ __forceinline__ int work_item(int bid, int total_items, int ipg) {
+__host__ __device__ __forceinline__ int work_item(int bid, int total_items, int ipg) {
   const int x = bid & 7, j = bid >> 3;
   const int groups = total_items / ipg;
   const int full_j = (groups / 8) * ipg;  // workgroups per XCD in whole rounds
