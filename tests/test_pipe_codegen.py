@@ -189,7 +189,7 @@ def test_checker_catches_planted_violations(plant):
         idx = next(i for i, ln in enumerate(body) if ln.startswith("v_mfma_f32_32x32x16_f16 v[16:31]"))
         bad = body[:idx] + [f"v_mul_f32 v16, %[al], v16"] + body[idx:]
     elif plant == "exp_then_use":
-        idx = next(i for i, ln in enumerate(body) if ln.startswith("v_exp_f32"))
+        idx = next(i for i, ln in enumerate(body) if ln.startswith("v_exp_f32 v"))
         r = _parse(body[idx])[1][0]
         bad = body[:idx + 1] + [f"v_mov_b32 v{G.T + 5}, {r}"] + body[idx + 1:]
     elif plant == "permlane_no_nop":
@@ -204,9 +204,13 @@ def test_checker_catches_planted_violations(plant):
         check_body(bad)
 
 
-OPTION_SETS = [{}, {"copy_at": 1}, {"skip_refill": True}, {"skip_rescale": True}, {"qk_il": True},
-               {"pv_il": True}, {"copy_at": 3, "skip_refill": True, "skip_rescale": True, "qk_il": True,
-                                 "pv_il": True}]
+_LEGACY = {"early": False, "v_ahead": False, "tail_first": False, "skip_refill": False}
+OPTION_SETS = [{}, _LEGACY, {**_LEGACY, "copy_at": 1}, {**_LEGACY, "skip_rescale": True},
+               {**_LEGACY, "qk_il": True}, {**_LEGACY, "pv_il": True}, {**_LEGACY, "early": True},
+               {**_LEGACY, "v_ahead": True}, {**_LEGACY, "tail_first": True}, {"skip_rescale": True},
+               {"qk_il": True, "pv_il": True}, {"auto_wait": True},
+               {"copy_at": 3, "skip_refill": True, "skip_rescale": True, "qk_il": True, "pv_il": True,
+                "early": False}]
 
 
 @pytest.fixture
@@ -245,6 +249,15 @@ def test_every_schedule_option_keeps_the_work(opts, option_set):
                     list(range(G.S16, G.S16 + 16)), name
     for mode in ("f16", "i8", "mixed"):
         check_m0(G.loop_asm(mode))
+
+
+def test_auto_wait_reproduces_the_hand_counted_waits(opts):
+    """With every read in its original place, the recomputed LDS waits equal
+    the counts the phase code writes by hand."""
+    opts.update(_LEGACY)
+    hand = G.generate()
+    opts["auto_wait"] = True
+    assert G.generate() == hand
 
 
 def test_bodies_read_operands_in_kstep_order():

@@ -66,6 +66,7 @@ starts with s_waitcnt lgkmcnt(0), and the scale loads are VMEM loads).
 """
 from __future__ import annotations
 
+import re
 import sys
 from pathlib import Path
 
@@ -92,8 +93,19 @@ K16_INS, K8_INS, V16_INS = 4, 2, 4  # 1 KB copies per wave and tile
 #   skip_rescale  the O rescale is skipped when alpha = 1 on every row of the
 #                 wave (an exact no-op then).
 #   qk_il         the two QK chains (kb 0, kb 1) alternate MFMA by MFMA;
-#   pv_il         the PV chains of d blocks (0, 1) and then (2, 3) alternate.
-OPTS = {"copy_at": None, "skip_refill": False, "skip_rescale": False, "qk_il": False, "pv_il": False}
+#   pv_il         the PV chains of d blocks (0, 1) and then (2, 3) alternate;
+#   early         the first four K operand reads go out right after the
+#                 barrier, before the tile copies (the drain: its first V
+#                 reads), so the copy issue covers their LDS latency;
+#   v_ahead       the first four PV operand reads go out beside the last four
+#                 QK MFMAs (their ring slots are free by then);
+#   tail_first    the last steps of the running maximum (m', alpha, -m') run
+#                 at the start of the next iteration, after its reads and
+#                 copies, instead of at the end of the body;
+#   auto_wait     LDS waits are recomputed from the operand registers (always
+#                 on with early / v_ahead).
+OPTS = {"copy_at": None, "skip_refill": True, "skip_rescale": False, "qk_il": False, "pv_il": False,
+        "early": True, "v_ahead": True, "tail_first": True, "auto_wait": False}
 
 
 def qk_step(i: int, nm: int) -> tuple[int, int]:
@@ -261,39 +273,118 @@ def spread(items: list[str], n: int) -> list[list[str]]:
 
 
 def phase_a(kind: str, kslot: int, valu: list[str], copy: list[str] | None = None,
-            tail: list[str] | None = None) -> list[str]:
+            tail: list[str] | None = None, pre: list[str] | None = None,
+            vslot: int | None = None) -> list[str]:
     """kind: 'f16' / 'i8' QK of the next tile, or 'none' (VALU only).  copy:
-    the tile copies, placed after MFMA OPTS['copy_at']; tail: after the last
-    chunk."""
-    copy, tail = copy or [], tail or []
+    the tile copies, placed after MFMA OPTS['copy_at'] (OPTS['early']: after
+    the first operand reads); pre: VALU work after the first reads and the
+    copies, before the first MFMA; tail: after the last chunk; vslot: the V
+    slot whose first PV operand reads go out beside the last four MFMAs."""
+    copy, tail, pre = copy or [], tail or [], pre or []
     if kind == "none":
-        return copy + list(valu) + tail
+        return copy + pre + list(valu) + tail
     nm = 16 if kind == "f16" else 8
     rd = read_k16 if kind == "f16" else read_k8
     mf = mfma_k16 if kind == "f16" else mfma_k8
+    early = OPTS["early"]
     out = [rd(i, kslot) for i in range(4)]
+    if early:
+        out += copy
+    out += pre
     chunks = spread(valu, nm)
     at = min(OPTS["copy_at"] or 0, nm - 1)
     for i in range(nm):
         out += [f"s_waitcnt lgkmcnt({min(3, nm - 1 - i)})", mf(i)]
         if i + 4 < nm:
             out.append(rd(i + 4, kslot))
-        if i == at:
+        elif vslot is not None:
+            out += reads_v(i - (nm - 4), vslot)
+        if i == at and not early:
             out += copy
         out += chunks[i]
     return out + tail
 
 
-def phase_b(vslot: int, chunks: list[list[str]], tail: list[str]) -> list[str]:
+def phase_b(vslot: int, chunks: list[list[str]], tail: list[str], pre_read: bool = False) -> list[str]:
+    """pre_read: the first four MFMAs' operand reads were issued earlier."""
     out: list[str] = []
-    for i in range(4):
-        out += reads_v(i, vslot)
+    if not pre_read:
+        for i in range(4):
+            out += reads_v(i, vslot)
     for i in range(16):
         out += [f"s_waitcnt lgkmcnt({min(6, 30 - 2 * i)})", mfma_pv(i)]
         if i + 4 < 16:
             out += reads_v(i + 4, vslot)
         out += chunks[i]
     return out + tail
+
+
+_REG = re.compile(r"v\[(\d+):(\d+)\]|\bv(\d+)\b")
+
+
+def _regs(tok: str) -> set[int]:
+    out: set[int] = set()
+    for m in _REG.finditer(tok):
+        if m.group(1) is not None:
+            out.update(range(int(m.group(1)), int(m.group(2)) + 1))
+        else:
+            out.add(int(m.group(3)))
+    return out
+
+
+def auto_wait(lines: list[str]) -> list[str]:
+    """The body's LDS waits, recomputed as the minimal ones: before an
+    instruction that reads or overwrites the destination of an outstanding
+    LDS read, wait until that read has returned (LDS reads return in order).
+    The full drain a body starts with is kept.  The only branches inside a
+    body skip blocks without LDS reads, so both paths see the same
+    outstanding reads."""
+    out: list[str] = []
+    pending: list[set[int]] = []
+    for k, ln in enumerate(lines):
+        if ln.startswith("s_waitcnt lgkmcnt("):
+            if k == 0:
+                out.append(ln)
+            continue
+        if ln.endswith(":") or ln.startswith("s_") or ln.startswith("buffer_"):
+            out.append(ln)
+            continue
+        op, _, rest = ln.partition(" ")
+        regs = _regs(rest)
+        hit = [j for j, d in enumerate(pending) if d & regs]
+        if hit:
+            j = max(hit)
+            out.append(f"s_waitcnt lgkmcnt({len(pending) - 1 - j})")
+            pending = pending[j + 1:]
+        out.append(ln)
+        if op.startswith("ds_read"):
+            pending.append(_regs(rest.split(",")[0]))
+    return out
+
+
+def pad_valu_mfma(lines: list[str]) -> list[str]:
+    """An s_nop before an MFMA that reads a register a VALU instruction wrote
+    fewer than three wait states earlier (each instruction is one wait
+    state, s_nop k is k + 1)."""
+    out: list[str] = []
+    written: dict[int, int] = {}  # register -> clock of its last VALU write
+    clock = 0
+    for ln in lines:
+        if ln.endswith(":"):
+            out.append(ln)
+            continue
+        op, _, rest = ln.partition(" ")
+        if op.startswith("v_mfma"):
+            gap = min((clock - written[r] for r in _regs(rest) if r in written), default=3)
+            if gap < 3:
+                out.append(f"s_nop {2 - gap}")
+                clock += 3 - gap
+        elif op.startswith("v_"):
+            for r in _regs(rest.split(",")[0]):
+                written[r] = clock
+        out.append(ln)
+        clock += int(rest) + 1 if op == "s_nop" else 1
+    return out
 
 
 def guard_rescale(lines: list[str], lbl: str) -> list[str]:
@@ -338,7 +429,7 @@ def b_chunks(kind: str, mixed_regs: bool, lbl: str) -> tuple[list[list[str]], li
         ch[13] += MAX_D
         ch[14] += MAX_E
         ch[15] += MAX_F
-        tail = list(MAX_TAIL)
+        tail = [] if OPTS["tail_first"] else list(MAX_TAIL)
         if mixed_regs:
             fa, fb = refill(QA), refill(QB)
             if OPTS["skip_refill"]:
@@ -354,19 +445,32 @@ def b_chunks(kind: str, mixed_regs: bool, lbl: str) -> tuple[list[list[str]], li
 
 def body_iter(kind: str, kslot: int, vslot: int, mixed_regs: bool, par_next: int, lbl: str = ".Lb",
               copy: list[str] | None = None) -> list[str]:
-    out = ["s_waitcnt lgkmcnt(0)"]
+    early, v_ahead = OPTS["early"], OPTS["v_ahead"] and kind != "none"
+    pre: list[str] = list(MAX_TAIL) if OPTS["tail_first"] else []
     if OPTS["skip_rescale"]:
-        out.append("v_cmp_neq_f32 vcc, 1.0, %[al]")
+        pre.append("v_cmp_neq_f32 vcc, 1.0, %[al]")
     if kind == "i8":
-        out += int8_scale(par_next)
+        pre += int8_scale(par_next)
+    out = ["s_waitcnt lgkmcnt(0)"]
+    if not early:
+        out, pre = out + pre, []
+    elif kind == "none":
+        # the drain computes no QK: its first PV operand reads go out first
+        for i in range(4):
+            out += reads_v(i, vslot)
+        out, pre, copy = out + (copy or []) + pre, [], None
+    vs = vslot if v_ahead else None
     if OPTS["pv_il"]:
-        out += phase_a(kind, kslot, softmax_steps() + rescale(0) + rescale(1), copy)
+        out += phase_a(kind, kslot, softmax_steps() + rescale(0) + rescale(1), copy, None, pre, vs)
     elif OPTS["skip_rescale"]:
-        out += phase_a(kind, kslot, softmax_steps(), copy, guard_rescale(rescale(0), f"{lbl}_rs0"))
+        out += phase_a(kind, kslot, softmax_steps(), copy, guard_rescale(rescale(0), f"{lbl}_rs0"), pre, vs)
     else:
-        out += phase_a(kind, kslot, softmax_steps() + rescale(0), copy)
+        out += phase_a(kind, kslot, softmax_steps() + rescale(0), copy, None, pre, vs)
     ch, tail = b_chunks(kind, mixed_regs, lbl)
-    return out + phase_b(vslot, ch, tail)
+    out += phase_b(vslot, ch, tail, pre_read=v_ahead or (early and kind == "none"))
+    if early or v_ahead or OPTS["auto_wait"]:
+        out = pad_valu_mfma(auto_wait(out))
+    return out
 
 
 def body_fill(kind: str, kslot: int, mixed_regs: bool, lbl: str = ".Lf") -> list[str]:
@@ -383,7 +487,9 @@ def body_fill(kind: str, kslot: int, mixed_regs: bool, lbl: str = ".Lf") -> list
             out += guard_refill(refill(QA) + refill(QB), f"{lbl}_rf")
         else:
             out += refill(QA) + refill(QB)
-    out += MAX_A + MAX_B + MAX_C + MAX_D + MAX_E + MAX_F + MAX_TAIL
+    out += MAX_A + MAX_B + MAX_C + MAX_D + MAX_E + MAX_F
+    if not OPTS["tail_first"]:
+        out += MAX_TAIL
     return out
 
 
@@ -474,7 +580,7 @@ def copies(mode: str, par: int, lbl: str) -> list[str]:
 def iteration(mode: str, par: int, lbl: str) -> list[str]:
     """Iteration n (n & 1 == par; %[n] holds n)."""
     mixed_regs = mode != "f16"
-    inner = OPTS["copy_at"] is not None
+    inner = OPTS["copy_at"] is not None or OPTS["early"]
     out = ["s_waitcnt vmcnt(0)", "s_barrier", "s_mov_b32 %[rn2], %[rn]"]
     if not inner:
         out += copies(mode, par, f"{lbl}_c")
