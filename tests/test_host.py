@@ -320,3 +320,29 @@ def test_int8_views_are_copied_to_16_byte_strides():
     # every int8 operand goes through the 16-byte rule before the launch
     assert "_inner_contiguous(v8, 16)" in src and "_inner_contiguous(k8, 16)" in src
     assert "_inner_contiguous(q8, 16)" in src
+
+
+def test_auto_routing_classification_is_cached_per_tensor_version(monkeypatch):
+    """routing_mode='auto' reads a bitmask back to the host once per tensor
+    and version: the same tensor again is not re-read, an in-place change or
+    another tensor with other bits is."""
+    calls = []
+    real = tmx.classify_bitmask_routing
+
+    def counting(t, **kw):
+        calls.append(1)
+        return real(t, **kw)
+
+    monkeypatch.setattr(tmx, "classify_bitmask_routing", counting)
+    kw = dict(seqlen_q=256, seqlen_k=256, block_m=128, block_n=64, block_n_mask=64, causal=True)
+    bm = torch.zeros(4, dtype=torch.uint64)
+    assert tmx._classify_cached(bm, **kw) == "fp16"
+    assert tmx._classify_cached(bm, **kw) == "fp16"
+    assert len(calls) == 1
+    bm.fill_(0xF)  # in place: version counter moves
+    assert tmx._classify_cached(bm, **kw) == "int8"
+    assert len(calls) == 2
+    other = torch.tensor([1, 0, 1, 0], dtype=torch.uint64)
+    assert tmx._classify_cached(other, **kw) == "mixed"
+    assert tmx._classify_cached(bm, **{**kw, "causal": False}) == real(bm, **{**kw, "causal": False})
+    assert len(calls) == 4
