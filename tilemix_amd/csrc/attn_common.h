@@ -146,6 +146,20 @@ __device__ __forceinline__ uint32_t pack_h2(float a, float b) {
   return __builtin_bit_cast(uint32_t, v);
 }
 
+// RN(h * s) for the low / high fp16 half of h2: the fp16 operand converts
+// exactly, so the product is rounded once, as RN(fp32(h) * s); the addend
+// -0 keeps the sign of a zero product.
+__device__ __forceinline__ float mul_lo(uint32_t h2, float s) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s), "v"(-0.0f));
+  return r;
+}
+__device__ __forceinline__ float mul_hi(uint32_t h2, float s) {
+  float r;
+  asm("v_fma_mix_f32 %0, %1, %2, %3 op_sel:[1,0,0] op_sel_hi:[1,0,0]" : "=v"(r) : "v"(h2), "v"(s), "v"(-0.0f));
+  return r;
+}
+
 // x / s correctly rounded, from r = RN(1/s): q0 = RN(x r), rem = x - q0 s
 // (exact, one FMA), RN(q0 + rem r) (Markstein's correction step).  For the
 // quantisation domain (x an fp16 value, s = RN(amax/127) with |x| <= amax, amax

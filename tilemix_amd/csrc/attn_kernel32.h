@@ -444,27 +444,44 @@ attn32_kernel(const AttnKArgs a) {
     for (int s = 0; s < KS16; ++s) qraw[s] = *reinterpret_cast<const f16x8*>(smem + STAGE + (qbase ^ (32 * s)));
   }
   if (MODE != TILEMIX_ROUTING_INT8) {
+    // fp16(RN(q * qk_scale)): one v_fma_mix per value (the fp16 operand
+    // converts exactly), then one packing conversion per pair.
 #pragma unroll
-    for (int s = 0; s < KS16; ++s)
+    for (int s = 0; s < KS16; ++s) {
+      const u32x4 w = __builtin_bit_cast(u32x4, qraw[s]);
+      u32x4 o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) qf[s][e] = (f16)fp32_round((float)qraw[s][e] * a.qk_scale);
+      for (int r = 0; r < 4; ++r) o[r] = pack_h2(mul_lo(w[r], a.qk_scale), mul_hi(w[r], a.qk_scale));
+      qf[s] = __builtin_bit_cast(f16x8, o);
+    }
   }
   if (q_fused) {
     // In-kernel Q quantisation (the workgroup's 128 rows are exactly one
     // BLKQ = 128 block of this head): scale = max|q| / 127 over the block's
     // rows inside the sequence, code = trunc(q / scale +- 0.5), the same
     // arithmetic as quant_per_block_int8 with sm_scale = 1.
-    float am = 0.0f;
+    // max|q| of the lane's 64 values as packed fp16 (exact: the maximum of
+    // magnitudes, sign bits cleared), then over the wave: lanes l ^ 32 and
+    // l ^ 16 by permlane swaps, the rest of a 16-lane row by DPP moves.
+    uint32_t hm = 0;
 #pragma unroll
-    for (int s = 0; s < KS16; ++s)
+    for (int s = 0; s < KS16; ++s) {
+      const u32x4 w = __builtin_bit_cast(u32x4, qraw[s]);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) am = fmaxf(am, fabsf((float)qraw[s][e]));
+      for (int r = 0; r < 4; ++r) hm = pk_max(hm, w[r] & 0x7fff7fffu);
+    }
+    const f16x2 hv = __builtin_bit_cast(f16x2, hm);
+    float am = fmaxf((float)hv[0], (float)hv[1]);
     {
       const float2 pr = swap_halves(am);
       am = fmaxf(pr.x, pr.y);
+      const float2 pq = pair16(am);
+      am = fmaxf(pq.x, pq.y);
     }
-#pragma unroll
-    for (int o = 16; o > 0; o >>= 1) am = fmaxf(am, __shfl_xor(am, o, 64));
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x128, 0xf, 0xf, false)));
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x124, 0xf, 0xf, false)));
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0x4e, 0xf, 0xf, false)));
+    am = fmaxf(am, __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(am), 0xb1, 0xf, 0xf, false)));
     if (lane == 0) q_red[wave] = am;
     __syncthreads();
     am = q_red[0];
@@ -488,10 +505,17 @@ attn32_kernel(const AttnKArgs a) {
       }
       const f16x8 xv = __builtin_bit_cast(f16x8, x), yv = __builtin_bit_cast(f16x8, y);
       uint32_t w[4] = {0u, 0u, 0u, 0u};
+      const u32x4 xw = __builtin_bit_cast(u32x4, xv), yw = __builtin_bit_cast(u32x4, yv);
 #pragma unroll
       for (int e = 0; e < 16; ++e) {
-        float t = div_by_recip((float)(e < 8 ? xv[e] : yv[e - 8]), qs, qr);
-        t += (t >= 0.0f) ? 0.5f : -0.5f;
+        // div_by_recip with q0 = RN(x r) straight from the fp16 operand
+        const uint32_t h2 = e < 8 ? xw[(e & 7) >> 1] : yw[(e & 7) >> 1];
+        const float x = (float)(e < 8 ? xv[e] : yv[e - 8]);
+        const float q0 = (e & 1) ? mul_hi(h2, qr) : mul_lo(h2, qr);
+        float t = __builtin_fmaf(__builtin_fmaf(-q0, qs, x), qr, q0);
+        // t + (t >= 0 ? 0.5 : -0.5); they differ only at t = -0, where both
+        // truncate to code 0
+        t += __builtin_copysignf(0.5f, t);
         const int code = (qs == 0.0f) ? 0 : (int)t;
         w[e >> 2] |= (uint32_t)(code & 0xff) << (8 * (e & 3));
       }
