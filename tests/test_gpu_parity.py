@@ -23,6 +23,7 @@ QUANT_CASES = [
     ("single256", [256], 4, 128),
     ("ragged", [1, 63, 64, 65, 300], 3, 128),
     ("with_empty", [1000, 0, 129], 2, 64),
+    ("d256_five_heads", [300, 20], 5, 256),  # blk 128 x d 256: the streamed (two-pass) path
 ]
 
 
