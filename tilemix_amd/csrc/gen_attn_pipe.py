@@ -13,19 +13,25 @@ of the next tile, m / alpha / -m / l) stays in fixed registers: the compiler
 moves values only at the statement's boundary.
 
 Iteration n (stage parity P = n & 1; tile t's K sits in K slot t & 1, its V in
-V slot t & 1):
+V slot t & 1), in the order of the default schedule options (OPTS below):
   1. s_waitcnt vmcnt(0) + s_barrier: this wave's copies of K(n+1) and V(n)
      have landed, every wave's have, and every wave is done with K(n) and
      V(n-1);
-  2. copies: K(n+2) into K slot P (with its route and K scale, while
+  2. the first four LDS operand reads of tile n+1's QK;
+  3. copies: K(n+2) into K slot P (with its route and K scale, while
      n+2 <= n_sw and n+2 < n_blocks) and V(n+1) into V slot 1-P;
-  3. phase A: QK MFMAs of tile n+1 (fp16: 16 x 32x32x16, int8: 8 x 32x32x32)
-     beside tile n's softmax, p = fp16(exp2(fp32(s) - m)), its row sum, and
-     the O rescale of d block 0;
-  4. phase B: PV MFMAs of tile n (16 x 32x32x16 f16) beside the rest of the O
-     rescale, the conversion of tile n+1's accumulators to fp16 scores (INT8
-     tiles: fma(acc bits, ss, -1.5 2^23 ss), the single rounding of acc * ss),
-     tile n+1's row maximum and alpha = exp2(m - m').
+  4. the last steps of tile n's running maximum: m' = max(m, mx),
+     alpha = exp2(min(m - mx, 0)), -m' (computed from the row maximum that
+     the previous body left in a temporary);
+  5. phase A: QK MFMAs of tile n+1 (fp16: 16 x 32x32x16, int8: 8 x 32x32x32)
+     beside tile n's softmax, p = fp16(exp2(fp32(s) - m')), its row sum, and
+     the O rescale of d block 0; the first PV operand reads go out beside
+     the last four QK MFMAs;
+  6. phase B: PV MFMAs of tile n (16 x 32x32x16 f16) beside the rest of the O
+     rescale, the l update, the conversion of tile n+1's accumulators to fp16
+     scores (INT8 tiles: fma(acc bits, ss, -1.5 2^23 ss), the single
+     rounding of acc * ss), the INT8 bias refill when the tile after next is
+     an INT8 tile, and tile n+1's packed row maximum.
 Before the loop, FILL runs tile 0's QK, conversion and maximum (after the
 barrier that also ends the Q block's use of stage 1, and the copy of K(1));
 the last iteration (DRAIN) has no next tile.  The C++ tile body continues at
@@ -58,11 +64,14 @@ addresses, copy descriptors and offsets, the route bits and counters).
 Hazards (gfx950; the compiler does not look inside the statement): an MFMA
 result is read by VALU code no sooner than ~18 instructions after the MFMA; a
 VALU write to an O block or to the INT8 accumulators precedes the MFMA that
-reads it by at least three instructions; an exp result is never read by the
-next instruction; v_permlane32_swap's operand is written two wait states
-earlier; one wait state separates an M0 write from the LDS-DMA copy that
-uses it.  LDS waits count only the statement's own reads (every compute block
-starts with s_waitcnt lgkmcnt(0), and the scale loads are VMEM loads).
+reads it by at least three wait states (pad_valu_mfma inserts the s_nop where
+the schedule does not provide them); an exp result is never read by the next
+instruction; v_permlane32_swap's operand is written two wait states earlier;
+one wait state separates an M0 write from the LDS-DMA copy that uses it.  LDS
+waits count only the statement's own reads (every compute body starts with
+s_waitcnt lgkmcnt(0), and the scale loads are VMEM loads); auto_wait derives
+them from the operand registers of each read's first use.
+tests/test_pipe_codegen.py replays every body against these rules.
 """
 from __future__ import annotations
 
