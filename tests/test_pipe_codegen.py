@@ -208,7 +208,7 @@ _LEGACY = {"early": False, "v_ahead": False, "tail_first": False, "skip_refill":
 OPTION_SETS = [{}, _LEGACY, {**_LEGACY, "copy_at": 1}, {**_LEGACY, "skip_rescale": True},
                {**_LEGACY, "qk_il": True}, {**_LEGACY, "pv_il": True}, {**_LEGACY, "early": True},
                {**_LEGACY, "v_ahead": True}, {**_LEGACY, "tail_first": True}, {"skip_rescale": True},
-               {"qk_il": True, "pv_il": True}, {"auto_wait": True},
+               {"qk_il": True, "pv_il": True}, {"auto_wait": True}, {"v_spread": True},
                {"copy_at": 3, "skip_refill": True, "skip_rescale": True, "qk_il": True, "pv_il": True,
                 "early": False}]
 
@@ -248,7 +248,11 @@ def test_every_schedule_option_keeps_the_work(opts, option_set):
                 assert sorted(int(ln.split()[1].rstrip(",")[1:]) for ln in conv) == \
                     list(range(G.S16, G.S16 + 16)), name
     for mode in ("f16", "i8", "mixed"):
-        check_m0(G.loop_asm(mode))
+        loop = G.loop_asm(mode)
+        check_m0(loop)
+        # every wave's share of a V tile is copied on each path of an iteration
+        if opts.get("v_spread"):
+            assert sum(ln.startswith("buffer_load_dwordx4 v153, %[rsv16]") for ln in loop) >= 4 * G.V16_INS
 
 
 def test_auto_wait_reproduces_the_hand_counted_waits(opts):

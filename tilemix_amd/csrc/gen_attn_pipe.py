@@ -112,9 +112,11 @@ K16_INS, K8_INS, V16_INS = 4, 2, 4  # 1 KB copies per wave and tile
 #                 at the start of the next iteration, after its reads and
 #                 copies, instead of at the end of the body;
 #   auto_wait     LDS waits are recomputed from the operand registers (always
-#                 on with early / v_ahead).
+#                 on with early / v_ahead);
+#   v_spread      in a body with a next tile, the four V copies go out one by
+#                 one after QK MFMAs 1, 3, 5 and 7 instead of with the K copy.
 OPTS = {"copy_at": None, "skip_refill": True, "skip_rescale": False, "qk_il": False, "pv_il": False,
-        "early": True, "v_ahead": True, "tail_first": True, "auto_wait": False}
+        "early": True, "v_ahead": True, "tail_first": True, "auto_wait": False, "v_spread": False}
 
 
 def qk_step(i: int, nm: int) -> tuple[int, int]:
@@ -283,7 +285,7 @@ def spread(items: list[str], n: int) -> list[list[str]]:
 
 def phase_a(kind: str, kslot: int, valu: list[str], copy: list[str] | None = None,
             tail: list[str] | None = None, pre: list[str] | None = None,
-            vslot: int | None = None) -> list[str]:
+            vslot: int | None = None, vgroups: list[list[str]] | None = None) -> list[str]:
     """kind: 'f16' / 'i8' QK of the next tile, or 'none' (VALU only).  copy:
     the tile copies, placed after MFMA OPTS['copy_at'] (OPTS['early']: after
     the first operand reads); pre: VALU work after the first reads and the
@@ -291,6 +293,7 @@ def phase_a(kind: str, kslot: int, valu: list[str], copy: list[str] | None = Non
     slot whose first PV operand reads go out beside the last four MFMAs."""
     copy, tail, pre = copy or [], tail or [], pre or []
     if kind == "none":
+        assert not vgroups
         return copy + pre + list(valu) + tail
     nm = 16 if kind == "f16" else 8
     rd = read_k16 if kind == "f16" else read_k8
@@ -310,6 +313,8 @@ def phase_a(kind: str, kslot: int, valu: list[str], copy: list[str] | None = Non
             out += reads_v(i - (nm - 4), vslot)
         if i == at and not early:
             out += copy
+        if vgroups and i % 2 == 1 and i // 2 < len(vgroups):
+            out += vgroups[i // 2]
         out += chunks[i]
     return out + tail
 
@@ -453,7 +458,7 @@ def b_chunks(kind: str, mixed_regs: bool, lbl: str) -> tuple[list[list[str]], li
 
 
 def body_iter(kind: str, kslot: int, vslot: int, mixed_regs: bool, par_next: int, lbl: str = ".Lb",
-              copy: list[str] | None = None) -> list[str]:
+              copy: list[str] | None = None, vgroups: list[list[str]] | None = None) -> list[str]:
     early, v_ahead = OPTS["early"], OPTS["v_ahead"] and kind != "none"
     pre: list[str] = list(MAX_TAIL) if OPTS["tail_first"] else []
     if OPTS["skip_rescale"]:
@@ -470,11 +475,12 @@ def body_iter(kind: str, kslot: int, vslot: int, mixed_regs: bool, par_next: int
         out, pre, copy = out + (copy or []) + pre, [], None
     vs = vslot if v_ahead else None
     if OPTS["pv_il"]:
-        out += phase_a(kind, kslot, softmax_steps() + rescale(0) + rescale(1), copy, None, pre, vs)
+        out += phase_a(kind, kslot, softmax_steps() + rescale(0) + rescale(1), copy, None, pre, vs, vgroups)
     elif OPTS["skip_rescale"]:
-        out += phase_a(kind, kslot, softmax_steps(), copy, guard_rescale(rescale(0), f"{lbl}_rs0"), pre, vs)
+        out += phase_a(kind, kslot, softmax_steps(), copy, guard_rescale(rescale(0), f"{lbl}_rs0"), pre, vs,
+                       vgroups)
     else:
-        out += phase_a(kind, kslot, softmax_steps() + rescale(0), copy, None, pre, vs)
+        out += phase_a(kind, kslot, softmax_steps() + rescale(0), copy, None, pre, vs, vgroups)
     ch, tail = b_chunks(kind, mixed_regs, lbl)
     out += phase_b(vslot, ch, tail, pre_read=v_ahead or (early and kind == "none"))
     if early or v_ahead or OPTS["auto_wait"]:
@@ -574,13 +580,29 @@ def copy_v(par: int) -> list[str]:
     return o + ["s_add_u32 %[tov16], %[tov16], %[tsv16]"]
 
 
-def copies(mode: str, par: int, lbl: str) -> list[str]:
+def copy_v_groups(par: int) -> list[list[str]]:
+    """copy_v split into its four copies (the offset advance goes with the last)."""
+    lines = copy_v(par)
+    groups: list[list[str]] = [[]]
+    for ln in lines:
+        groups[-1].append(ln)
+        if ln.startswith("buffer_load"):
+            groups.append([])
+    tail = groups.pop()
+    groups[-1] += tail
+    assert len(groups) == V16_INS
+    return groups
+
+
+def copies(mode: str, par: int, lbl: str, with_v: bool = True) -> list[str]:
     """Iteration n's copies: K(n+2) while n + 2 <= n_sw and n + 2 < n_blocks
     (its route -> %[rn2]), V(n+1) while n + 1 < n_blocks."""
     out = ["s_add_u32 %[t], %[n], 2", "s_cmp_gt_u32 %[t], %[nsw]", f"s_cbranch_scc1 {lbl}_nok",
            "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nok"]
     out += copy_k(mode, par, f"{lbl}_ck")
     out += ["s_mov_b32 %[rn2], %[r2]", f"{lbl}_nok:"]
+    if not with_v:
+        return out
     out += ["s_add_u32 %[t], %[n], 1", "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nov"]
     out += copy_v(par)
     return out + [f"{lbl}_nov:"]
@@ -597,13 +619,16 @@ def iteration(mode: str, par: int, lbl: str) -> list[str]:
     out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {lbl}_inact",
             "s_add_u32 %[t], %[n], 1", "s_cmp_ge_u32 %[t], %[nsw]", f"s_cbranch_scc1 {lbl}_drain"]
 
-    def cp(tag: str) -> list[str] | None:
-        return copies(mode, par, f"{lbl}_{tag}c") if inner else None
+    def cp(tag: str, with_v: bool = True) -> list[str] | None:
+        return copies(mode, par, f"{lbl}_{tag}c", with_v) if inner else None
 
+    # a body with a next tile always copies V(n+1) (n + 1 < n_sw <= n_blocks)
+    vsp = OPTS["v_spread"] and inner
+    vg = copy_v_groups(par) if vsp else None
     if mode in ("f16", "mixed"):
-        f16_body = body_iter("f16", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_f", cp("f"))
+        f16_body = body_iter("f16", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_f", cp("f", not vsp), vg)
     if mode in ("i8", "mixed"):
-        i8_body = body_iter("i8", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_i", cp("i"))
+        i8_body = body_iter("i8", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_i", cp("i", not vsp), vg)
     if mode == "f16":
         out += f16_body
     elif mode == "i8":
