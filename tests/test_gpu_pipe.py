@@ -117,3 +117,38 @@ def test_pipe_matches_oracle(device, case):
                      blkk=blkk)
     mx, mean = assert_close_out(got, ref)
     print(f"pipe vs oracle {name}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+
+
+def _random_case(seed):
+    """A seeded random launch of the pipelined instantiations: 1-4 ragged
+    sequences (some shorter than a tile, some empty), GQA 1-4, head_dim
+    65-128, block_m 128 or 256, causal or not, any routing mode and map."""
+    rng = np.random.default_rng(1000 + seed)
+    nseq = int(rng.integers(1, 5))
+    lq = [int(x) for x in rng.integers(0, 1100, size=nseq)]
+    lq[int(rng.integers(0, nseq))] = int(rng.integers(300, 1100))
+    causal = bool(rng.integers(0, 2))
+    lk = None if causal or rng.integers(0, 2) == 0 else [int(x) for x in rng.integers(1, 1100, size=nseq)]
+    if lk is not None:
+        lk[int(np.argmax(lq))] = max(lk[int(np.argmax(lq))], max(lq))  # keep one max length for Q and K
+    hk = int(rng.integers(1, 3))
+    group = int(rng.choice([1, 2, 3, 4]))
+    d = int(rng.choice([72, 96, 112, 128]))
+    block_m = int(rng.choice([128, 128, 256]))
+    bnm = int(rng.choice([64, 128]))
+    mode = str(rng.choice(["mixed", "mixed", "fp16", "int8"]))
+    blkk = int(rng.choice([64, 128]))
+    return (f"random{seed}", lq, lk, hk * group, hk, d, block_m, bnm, causal, mode, "rand", blkk)
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_pipe_random_launches_bitwise(device, seed):
+    case = _random_case(seed)
+    name = case[0]
+    inputs = _inputs(case, 17 + seed)
+    ref = _launch(device, inputs, case, pipe=False)
+    got = _launch(device, inputs, case, pipe=True)
+    same = got.view(np.uint16) == ref.view(np.uint16)
+    print(f"pipe vs C++ body {case}: {same.mean():.6f} identical", flush=True)
+    assert np.isfinite(got).all()
+    assert same.all(), (name, np.argwhere(~same)[:5])
