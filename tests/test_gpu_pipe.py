@@ -9,6 +9,9 @@ and two pipelined tiles (FILL then DRAIN at once), odd and even counts (both
 unrolled parities end the loop), ragged and empty sequences in one launch,
 the causal diagonal and a ragged end handed to the C++ body, Lq != Lk, mask
 groups of two tiles, block_m 256 (routing rows shared by two workgroups),
+block_m 64 with mixed routing (split workgroups: the two 64-row halves route
+separately, and a tile past the low half's last key copies only the high
+half's K format),
 head_dim 80 and 96 (zero-padded columns), MHA and GQA 4, each routing mode,
 and the INT8 scale bookkeeping at BLKK 128 / 256 (scale blocks spanning tiles).
 """
@@ -44,6 +47,15 @@ CASES = [
     ("blkk128", [900, 130], None, 4, 2, 128, 128, 64, True, "mixed", "rand", 128),
     ("blkk256_int8", [1000], None, 2, 1, 128, 128, 64, True, "int8", "rand", 256),
     ("fp16_bm64", [333, 64], None, 4, 2, 128, 64, 64, True, "fp16", "rand", 64),
+    # block_m 64 with mixed routing: split workgroups (per-half routes, both K formats per stage)
+    ("split_sptrans", [2048], None, 3, 1, 128, 64, 64, True, "mixed", "sptrans", 64),
+    ("split_short_and_ragged", [1, 63, 64, 65, 127, 129, 191, 257, 0, 700], None, 4, 2, 128, 64, 64, True,
+     "mixed", "rand", 64),
+    ("split_lq_lt_lk", [100, 300, 64], [400, 1000, 64], 4, 2, 128, 64, 64, True, "mixed", "rand", 64),
+    ("split_lq_gt_lk", [600, 300], [200, 299], 4, 2, 128, 64, 64, True, "mixed", "rand", 64),
+    ("split_noncausal", [300, 450], [333, 513], 2, 2, 128, 64, 64, False, "mixed", "rand", 64),
+    ("split_group2_blkk128", [900, 130], None, 4, 2, 128, 64, 128, True, "mixed", "rand", 128),
+    ("split_hd96_gqa3", [640], None, 6, 2, 96, 64, 64, True, "mixed", "rand", 64),
 ]
 
 
@@ -103,7 +115,8 @@ def test_pipe_bitwise_equals_cpp_body(device, case):
 
 
 @pytest.mark.parametrize("case", [c for c in CASES if c[0] in ("short_and_ragged", "lq_lt_lk", "blkk128",
-                                                               "sptrans", "hd80_mha")],
+                                                               "sptrans", "hd80_mha", "split_short_and_ragged",
+                                                               "split_sptrans")],
                          ids=lambda c: c[0])
 def test_pipe_matches_oracle(device, case):
     name, lq, lk, hq, hk, d, block_m, bnm, causal, mode, kind, blkk = case
@@ -119,11 +132,12 @@ def test_pipe_matches_oracle(device, case):
     print(f"pipe vs oracle {name}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
 
 
-def _random_case(seed):
+def _random_case(seed, split=False):
     """A seeded random launch of the pipelined instantiations: 1-4 ragged
     sequences (some shorter than a tile, some empty), GQA 1-4, head_dim
-    65-128, block_m 128 or 256, causal or not, any routing mode and map."""
-    rng = np.random.default_rng(1000 + seed)
+    65-128, block_m 128 or 256, causal or not, any routing mode and map
+    (split: block_m 64 with mixed routing)."""
+    rng = np.random.default_rng((2000 if split else 1000) + seed)
     nseq = int(rng.integers(1, 5))
     lq = [int(x) for x in rng.integers(0, 1100, size=nseq)]
     lq[int(rng.integers(0, nseq))] = int(rng.integers(300, 1100))
@@ -138,7 +152,10 @@ def _random_case(seed):
     bnm = int(rng.choice([64, 128]))
     mode = str(rng.choice(["mixed", "mixed", "fp16", "int8"]))
     blkk = int(rng.choice([64, 128]))
-    return (f"random{seed}", lq, lk, hk * group, hk, d, block_m, bnm, causal, mode, "rand", blkk)
+    if split:
+        block_m, mode = 64, "mixed"
+    return (f"random{'_split' if split else ''}{seed}", lq, lk, hk * group, hk, d, block_m, bnm, causal, mode,
+            "rand", blkk)
 
 
 @pytest.mark.parametrize("seed", range(8))
@@ -146,6 +163,19 @@ def test_pipe_random_launches_bitwise(device, seed):
     case = _random_case(seed)
     name = case[0]
     inputs = _inputs(case, 17 + seed)
+    ref = _launch(device, inputs, case, pipe=False)
+    got = _launch(device, inputs, case, pipe=True)
+    same = got.view(np.uint16) == ref.view(np.uint16)
+    print(f"pipe vs C++ body {case}: {same.mean():.6f} identical", flush=True)
+    assert np.isfinite(got).all()
+    assert same.all(), (name, np.argwhere(~same)[:5])
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_pipe_random_split_launches_bitwise(device, seed):
+    case = _random_case(seed, split=True)
+    name = case[0]
+    inputs = _inputs(case, 41 + seed)
     ref = _launch(device, inputs, case, pipe=False)
     got = _launch(device, inputs, case, pipe=True)
     same = got.view(np.uint16) == ref.view(np.uint16)

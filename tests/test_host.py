@@ -346,3 +346,24 @@ def test_auto_routing_classification_is_cached_per_tensor_version(monkeypatch):
     assert tmx._classify_cached(other, **kw) == "mixed"
     assert tmx._classify_cached(bm, **{**kw, "causal": False}) == real(bm, **{**kw, "causal": False})
     assert len(calls) == 4
+
+
+def test_placeholder_metadata_shapes_and_sharing():
+    """The all-FP16 / fp16-V placeholders keep the reference's shapes, dtypes
+    and zero scale prefixes (attention/triton/tilemix.py:1087-1129), and are
+    created once: a second call returns the same tensors (no fill per call)."""
+    q = torch.zeros((300, 6, 128), dtype=torch.float16)
+    k = torch.zeros((300, 2, 128), dtype=torch.float16)
+    cu = torch.tensor([0, 100, 300], dtype=torch.int32)
+    v8, sv, cuv = tmx._dummy_v_quantization_metadata(k, cu)
+    assert v8.shape == (1, 2, 128) and v8.dtype == torch.int8
+    assert sv.shape == (1, 2) and sv.dtype == torch.float16
+    assert cuv.shape == cu.shape and cuv.dtype == torch.int32 and not cuv.any()
+    again = tmx._dummy_v_quantization_metadata(k, cu)
+    assert all(a is b for a, b in zip((v8, sv, cuv), again))
+    q8, sq, cuq, k8, sk, cuk, v8b, svb, cuvb = tmx._dummy_quantization_metadata(q, k, k, cu, cu)
+    assert q8.shape == (1, 6, 128) and k8.shape == (1, 2, 128) and v8b.shape == (1, 2, 128)
+    assert sq.shape == (1, 6) and sk.shape == (1, 2) and svb.shape == (1, 2)
+    assert all(t.dtype == torch.int32 and t.shape == cu.shape and not t.any() for t in (cuq, cuk, cuvb))
+    other = tmx._dummy_v_quantization_metadata(k, torch.tensor([0, 300], dtype=torch.int32))
+    assert other[2].shape == (2,) and other[2] is not cuv

@@ -161,9 +161,121 @@ def test_body_hazards(name):
     check_body(BODIES[name])
 
 
-@pytest.mark.parametrize("mode", ["f16", "i8", "mixed"])
+@pytest.mark.parametrize("mode", ["f16", "i8", "mixed", "split"])
 def test_loop_m0_rule(mode):
     check_m0(G.loop_asm(mode))
+
+
+@pytest.mark.parametrize("mode", ["f16", "i8", "mixed", "split"])
+def test_lds_offsets_fit_and_stay_in_the_stages(mode):
+    """Every LDS read offset fits the 16-bit field; every copy destination
+    (M0 offset + this wave's 1 KB) lies inside the two stages, in the slot of
+    its stream."""
+    stage = G.SPLIT_STAGE if mode == "split" else G.STAGE
+    k8off = G.SPLIT_K8OFF if mode == "split" else 0
+    loop = G.loop_asm(mode)
+    for ln in loop:
+        m = re.search(r"offset:(\d+)$", ln)
+        if ln.startswith("ds_read") and m:
+            assert int(m.group(1)) < 1 << 16, ln
+    dest = None
+    for ln in loop:
+        m = re.match(r"s_add_u32 m0, %\[ldsw\], (\d+)$", ln)
+        if m:
+            dest = int(m.group(1))
+        elif ln.startswith("buffer_load_dwordx4") and ln.endswith("lds"):
+            stream = re.search(r"%\[(rs\w+)\]", ln).group(1)
+            par, off = divmod(dest, stage)
+            assert par in (0, 1) and off + G.NW * 1024 <= stage, ln
+            lo, size = {"rsk16": (0, 64 * G.ROW16), "rsk8": (k8off, 64 * G.ROW8),
+                        "rsv16": (G.VOFF, 64 * G.ROW16)}[stream]
+            assert lo <= off and off + G.NW * 1024 <= lo + size, (ln, dest)
+
+
+def _salu_route(lines, regs):
+    """Runs the SALU route computation of a K copy (the lines up to the route
+    group advance) and returns %[r2]."""
+    scc, i = 0, 0
+    labels = {ln[:-1]: j for j, ln in enumerate(lines) if ln.endswith(":")}
+    val = lambda a: regs[a[2:-1]] if a.startswith("%[") else int(a)
+    while i < len(lines):
+        ln = lines[i]
+        i += 1
+        if ln.endswith(":"):
+            continue
+        op, args = _parse(ln)
+        if op == "s_add_u32" and args[0] == "%[gc]":
+            break
+        if op in ("s_bitcmp1_b64", "s_bitcmp1_b32"):
+            scc = (val(args[0]) >> val(args[1])) & 1
+        elif op == "s_cselect_b32":
+            regs[args[0][2:-1]] = val(args[1]) if scc else val(args[2])
+        elif op == "s_cmp_ge_u32":
+            scc = int(val(args[0]) >= val(args[1]))
+        elif op == "s_cbranch_scc1":
+            if scc:
+                i = labels[args[0]]
+        elif op == "s_and_b32":
+            regs[args[0][2:-1]] = val(args[1]) & val(args[2])
+        elif op == "s_or_b32":
+            regs[args[0][2:-1]] = val(args[1]) | val(args[2])
+        elif op == "s_mov_b32":
+            regs[args[0][2:-1]] = val(args[1])
+        else:
+            raise AssertionError(f"unexpected instruction in the route block: {ln}")
+    return regs["r2"]
+
+
+def test_split_route_matches_the_kernels_tile_route():
+    """The split loop's route of a copied tile, run instruction by
+    instruction, equals attn_kernel32.h's tile_route for SPLIT: bit 1 the high
+    half's bit of the route group, bit 0 the low half's unless the tile starts
+    past the low half's last key (t * 64 > lo_last_key, i.e. t >= lolim)."""
+    import random
+    with G.layout("split"):
+        lines = G.copy_k("split", 0, ".Lt")
+
+    def mismatches(route_lines, lolim_of=lambda lk: 0 if lk < 0 else lk // 64 + 1):
+        rnd = random.Random(7)
+        bad = 0
+        for _ in range(3000):
+            bits, bitsh = rnd.getrandbits(64), rnd.getrandbits(64)
+            t, grp = rnd.randrange(64), rnd.randrange(64)
+            lo_last_key = rnd.randrange(-200, 64 * 64)
+            rhi = (bitsh >> grp) & 1
+            rlo = rhi if t * 64 > lo_last_key else (bits >> grp) & 1
+            regs = {"bits": bits, "bitsh": bitsh, "grp": grp, "t": t, "lolim": lolim_of(lo_last_key)}
+            bad += _salu_route(route_lines, regs) != rlo | (rhi << 1)
+        return bad
+
+    assert mismatches(lines) == 0
+    # planted mistakes: the halves' words swapped, the limit off by one tile
+    swapped = [ln.replace("%[bitsh]", "%[X]").replace("%[bits]", "%[bitsh]").replace("%[X]", "%[bits]")
+               for ln in lines]
+    assert mismatches(swapped) > 0
+    assert mismatches(lines, lambda lk: 0 if lk < 0 else lk // 64) > 0
+
+
+def test_split_loop_formats_and_wave_bits():
+    """split: fp16 K is copied unless both halves are INT8 and int8 K unless
+    both are FP16; each compute branch and refill guard tests this wave's bit
+    of the two-bit route, never the whole route."""
+    loop = G.loop_asm("split")
+    text = "\n".join(loop)
+    assert "s_cmp_eq_u32 %[rn], 0" not in text and "s_cmp_eq_u32 %[rn2], 0" not in text
+    assert sum(ln == "s_bitcmp1_b32 %[rn], %[half]" for ln in loop) == \
+        sum(ln == "s_cmp_eq_u32 %[rn], 0" for ln in G.loop_asm("mixed"))
+    assert sum(ln == "s_bitcmp0_b32 %[rn2], %[half]" for ln in loop) == \
+        sum(ln == "s_cmp_eq_u32 %[rn2], 0" for ln in G.loop_asm("mixed"))
+    with G.layout("split"):
+        ck = G.copy_k("split", 1, ".Lt")
+    i16 = ck.index("s_cmp_eq_u32 %[r2], 3")
+    i8 = ck.index("s_cmp_eq_u32 %[r2], 0")
+    assert i16 < i8
+    assert all("rsk16" not in ln for ln in ck[i8:]) and any("rsk8" in ln for ln in ck[i8:])
+    assert any("buffer_load_ushort" in ln for ln in ck[i8:])
+    # the generated header carries the split loop and restores the default layout
+    assert "pipe_loop_split" in G.generate() and G.LAYOUT["stage"] == G.STAGE
 
 
 def _planted(lines, pred, repl):
@@ -247,7 +359,7 @@ def test_every_schedule_option_keeps_the_work(opts, option_set):
             if not name.startswith("drain"):
                 assert sorted(int(ln.split()[1].rstrip(",")[1:]) for ln in conv) == \
                     list(range(G.S16, G.S16 + 16)), name
-    for mode in ("f16", "i8", "mixed"):
+    for mode in ("f16", "i8", "mixed", "split"):
         loop = G.loop_asm(mode)
         check_m0(loop)
         # every wave's share of a V tile is copied on each path of an iteration

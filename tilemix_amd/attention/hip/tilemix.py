@@ -188,26 +188,47 @@ def _forced_config_check(block_m: int, block_n: int) -> None:
             f"forced=({forced_m}, {forced_n}), requested=({block_m}, {block_n})")
 
 
+_PLACEHOLDERS: dict = {}
+
+
+def _placeholder(kind: str, shape: tuple, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """A placeholder quantisation tensor, created once per (kind, shape, dtype,
+    device) and shared by every later call.  The kernel never reads or writes
+    the placeholders of an unquantised operand, so sharing them is safe, and
+    the zero-filled scale prefixes then cost no fill kernel per call (a
+    per-call fill put a ~2-5 us kernel into every step)."""
+    key = (kind, tuple(shape), dtype, device)
+    t = _PLACEHOLDERS.get(key)
+    if t is None:
+        if len(_PLACEHOLDERS) >= 256:
+            _PLACEHOLDERS.clear()
+        t = (torch.zeros if kind == "zeros" else torch.empty)(shape, dtype=dtype, device=device)
+        _PLACEHOLDERS[key] = t
+    return t
+
+
 def _dummy_quantization_metadata(q, k, v, cu_seqlens_q, cu_seqlens_k):
-    """Reference :1087-1115 -- placeholders for the all-FP16 mode."""
+    """Reference :1087-1115 -- placeholders for the all-FP16 mode (shared
+    between calls: the kernel reads none of them in that mode)."""
     dev = q.device
-    q8 = torch.empty((1, q.shape[1], q.shape[2]), dtype=torch.int8, device=dev)
-    k8 = torch.empty((1, k.shape[1], k.shape[2]), dtype=torch.int8, device=dev)
-    v8 = torch.empty((1, v.shape[1], v.shape[2]), dtype=torch.int8, device=dev)
-    sq = torch.empty((1, q.shape[1]), dtype=q.dtype, device=dev)
-    sk = torch.empty((1, k.shape[1]), dtype=k.dtype, device=dev)
-    sv = torch.empty_like(sk)
-    cuq = torch.zeros_like(cu_seqlens_q, dtype=torch.int32, device=dev)
-    cuk = torch.zeros_like(cu_seqlens_k, dtype=torch.int32, device=dev)
-    cuv = torch.zeros_like(cu_seqlens_k, dtype=torch.int32, device=dev)
+    q8 = _placeholder("empty", (1, q.shape[1], q.shape[2]), torch.int8, dev)
+    k8 = _placeholder("empty", (1, k.shape[1], k.shape[2]), torch.int8, dev)
+    v8 = _placeholder("empty", (1, v.shape[1], v.shape[2]), torch.int8, dev)
+    sq = _placeholder("empty", (1, q.shape[1]), q.dtype, dev)
+    sk = _placeholder("empty", (1, k.shape[1]), k.dtype, dev)
+    sv = sk
+    cuq = _placeholder("zeros", tuple(cu_seqlens_q.shape), torch.int32, dev)
+    cuk = _placeholder("zeros", tuple(cu_seqlens_k.shape), torch.int32, dev)
+    cuv = cuk
     return q8, sq, cuq, k8, sk, cuk, v8, sv, cuv
 
 
 def _dummy_v_quantization_metadata(v, cu_seqlens_k):
-    """Reference :1118-1129."""
-    v8 = torch.empty((1, v.shape[1], v.shape[2]), dtype=torch.int8, device=v.device)
-    sv = torch.empty((1, v.shape[1]), dtype=v.dtype, device=v.device)
-    cuv = torch.zeros_like(cu_seqlens_k, dtype=torch.int32, device=v.device)
+    """Reference :1118-1129 (placeholders shared between calls: with fp16 V the
+    kernel reads none of them)."""
+    v8 = _placeholder("empty", (1, v.shape[1], v.shape[2]), torch.int8, v.device)
+    sv = _placeholder("empty", (1, v.shape[1]), v.dtype, v.device)
+    cuv = _placeholder("zeros", tuple(cu_seqlens_k.shape), torch.int32, v.device)
     return v8, sv, cuv
 
 

@@ -60,8 +60,8 @@ template <int NW, int DP, int MODE, bool INT8V, bool DUMP, bool BIAS, bool SPLIT
 __global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(2, 2)))
 attn32_kernel(const AttnKArgs a) {
   static_assert(!SPLIT || (NW % 2 == 0 && !INT8V), "split workgroups: even wave count, fp16 V");
-  static_assert(!PIPE || (NW == 4 && DP == 128 && !INT8V && !DUMP && !BIAS && !SPLIT && !GEN),
-                "the pipelined tile body serves the plain 4-wave head_dim-128 launch");
+  static_assert(!PIPE || (NW == 4 && DP == 128 && !INT8V && !DUMP && !BIAS && !GEN),
+                "the pipelined tile body serves the plain and split 4-wave head_dim-128 launches");
   constexpr int BM = NW * 32;
   // K/V scales per tile and lane: one, or (GEN) one per 4-key group g = 4 kb + jj
   // of the lane's keys 32 kb + 8 jj + 4 hi .. + 3.
@@ -848,7 +848,7 @@ attn32_kernel(const AttnKArgs a) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) po.k8a[ks] = (int)smem_lds + K8OFF + (kb8 ^ (32 * ks));
 #pragma unroll
-      for (int db = 0; db < 4; ++db) po.va[db] = (int)smem_lds + (vb ^ (64 * db));
+      for (int db = 0; db < 4; ++db) po.va[db] = (int)smem_lds + KBUF + (vb ^ (64 * db));
       if constexpr (MODE != TILEMIX_ROUTING_INT8) {
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) po.qf[ks] = qf[ks];
@@ -873,6 +873,10 @@ attn32_kernel(const AttnKArgs a) {
       c.nblk = n_blocks;
       c.act = row0w < Lq ? 1 : 0;
       c.bits = bits;
+      c.bits_hi = bits_hi;
+      // split: tile t lies past the low half's last key iff t * 64 > lo_last_key
+      c.lolim = lo_last_key < 0 ? 0 : lo_last_key / kBN + 1;
+      c.half = half;
       c.mt = a.mask_tiles;
       c.kbt = kb_tiles;
       c.hask = has_ks ? 1 : 0;
@@ -915,6 +919,7 @@ attn32_kernel(const AttnKArgs a) {
         c.tok16 = u(c.tok16); c.tok8 = u(c.tok8); c.tov16 = u(c.tov16);
         c.grp = u(c.grp); c.gc = u(c.gc); c.sc = u(c.sc); c.skoff = u(c.skoff); c.rn = u(c.rn);
         c.nsw = u(c.nsw); c.nblk = u(c.nblk); c.act = u(c.act); c.bits = u64(c.bits);
+        c.bits_hi = u64(c.bits_hi); c.lolim = u(c.lolim); c.half = u(c.half);
         c.mt = u(c.mt); c.kbt = u(c.kbt); c.hask = u(c.hask); c.sklast = u(c.sklast); c.hk2 = u(c.hk2);
         c.rssk = u4(c.rssk); c.rsk16 = u4(c.rsk16); c.rsk8 = u4(c.rsk8); c.rsv16 = u4(c.rsv16);
         c.stpk16 = u(c.stpk16); c.stpk8 = u(c.stpk8); c.stpv16 = u(c.stpv16);
@@ -923,6 +928,7 @@ attn32_kernel(const AttnKArgs a) {
       }
       if constexpr (MODE == TILEMIX_ROUTING_FP16) pipe_loop_f16(st, po, c);
       else if constexpr (MODE == TILEMIX_ROUTING_INT8) pipe_loop_i8(st, po, c);
+      else if constexpr (SPLIT) pipe_loop_split(st, po, c);
       else pipe_loop_mixed(st, po, c);
 
 #pragma unroll

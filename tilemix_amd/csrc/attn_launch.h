@@ -20,6 +20,13 @@ struct AttnLauncher {
     }
     if constexpr (MODE == TILEMIX_ROUTING_MIXED && !INT8V) {
       if (kind == kAttn32Split) {
+        if constexpr (DP == 128 && !DUMP && !BIAS && !GEN) {
+          if (a.pipe) {
+            hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, true, GEN, true>), grid, block, 0,
+                               stream, a);
+            return;
+          }
+        }
         hipLaunchKernelGGL((attn32_kernel<4, DP, MODE, INT8V, DUMP, BIAS, true, GEN>), grid, block, 0, stream, a);
         return;
       }

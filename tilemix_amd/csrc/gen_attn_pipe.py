@@ -10,7 +10,10 @@ tiles, fp16 V, and the tiles [0, n_sw) that need no mask for any row of the
 workgroup.  The whole loop over those tiles is ONE inline-assembly statement
 (pipe_loop_<mode>), so the loop-carried state (the O accumulators, the scores
 of the next tile, m / alpha / -m / l) stays in fixed registers: the compiler
-moves values only at the statement's boundary.
+moves values only at the statement's boundary.  Modes: f16, i8 and mixed
+routing, and split (mixed routing at block_m 64: the workgroup's two 64-row
+halves route separately, a 40 KB stage holds K in both formats when their
+routes differ, and each wave takes its own half's route).
 
 Iteration n (stage parity P = n & 1; tile t's K sits in K slot t & 1, its V in
 V slot t & 1), in the order of the default schedule options (OPTS below):
@@ -77,6 +80,7 @@ from __future__ import annotations
 
 import re
 import sys
+from contextlib import contextmanager
 from pathlib import Path
 
 ACC = (0, 16, 32, 48)
@@ -90,6 +94,9 @@ SS, NMS = 151, 152
 VO = 153
 STAGE = 32768  # bytes per LDS stage (K 16 KB + V 16 KB)
 VOFF = 16384   # V slot offset inside a stage
+# Split workgroups (block_m 64: the two 64-row halves route separately): a
+# stage holds K in both formats, int8 K after V.
+SPLIT_STAGE, SPLIT_K8OFF = 40960, 32768
 ROW16, ROW8 = 256, 128
 NW = 4
 K16_INS, K8_INS, V16_INS = 4, 2, 4  # 1 KB copies per wave and tile
@@ -117,6 +124,24 @@ K16_INS, K8_INS, V16_INS = 4, 2, 4  # 1 KB copies per wave and tile
 #                 one after QK MFMAs 1, 3, 5 and 7 instead of with the K copy.
 OPTS = {"copy_at": None, "skip_refill": True, "skip_rescale": False, "qk_il": False, "pv_il": False,
         "early": True, "v_ahead": True, "tail_first": True, "auto_wait": False, "v_spread": False}
+
+# The launch the loop is generated for (loop_asm sets it per mode): the stage
+# size, the int8 K offset inside a stage, and whether routes are per half
+# (split: %[rn] / %[rn2] carry the low half's route in bit 0 and the high
+# half's in bit 1, and each wave tests bit %[half]).
+LAYOUT = {"stage": STAGE, "k8off": 0, "split": False}
+
+
+@contextmanager
+def layout(mode: str):
+    saved = dict(LAYOUT)
+    if mode == "split":
+        LAYOUT.update(stage=SPLIT_STAGE, k8off=SPLIT_K8OFF, split=True)
+    try:
+        yield
+    finally:
+        LAYOUT.clear()
+        LAYOUT.update(saved)
 
 
 def qk_step(i: int, nm: int) -> tuple[int, int]:
@@ -146,12 +171,12 @@ def slot(i: int) -> str:
 
 def read_k16(i: int, kslot: int) -> str:
     kb, ks = qk_step(i, 16)
-    return f"ds_read_b128 {slot(i)}, %[ka{ks}] offset:{kslot * STAGE + kb * 32 * ROW16}"
+    return f"ds_read_b128 {slot(i)}, %[ka{ks}] offset:{kslot * LAYOUT['stage'] + kb * 32 * ROW16}"
 
 
 def read_k8(i: int, kslot: int) -> str:
     kb, ks = qk_step(i, 8)
-    return f"ds_read_b128 {slot(i)}, %[k8a{ks}] offset:{kslot * STAGE + kb * 32 * ROW8}"
+    return f"ds_read_b128 {slot(i)}, %[k8a{ks}] offset:{kslot * LAYOUT['stage'] + kb * 32 * ROW8}"
 
 
 def mfma_k16(i: int) -> str:
@@ -173,7 +198,7 @@ def reads_v(i: int, vslot: int) -> list[str]:
     db, ks = pv_step(i)
     base = RING + 4 * (i % 4)
     return [f"ds_read_b64_tr_b16 {vr(base + 2 * h2, 2)}, %[va{db}] "
-            f"offset:{vslot * STAGE + VOFF + (16 * ks + 8 * h2) * ROW16}" for h2 in range(2)]
+            f"offset:{vslot * LAYOUT['stage'] + (16 * ks + 8 * h2) * ROW16}" for h2 in range(2)]
 
 
 def mfma_pv(i: int) -> str:
@@ -408,8 +433,18 @@ def guard_rescale(lines: list[str], lbl: str) -> list[str]:
 
 
 def guard_refill(lines: list[str], lbl: str) -> list[str]:
-    """Skip an accumulator refill when the tile after next is an FP16 tile."""
-    return ["s_cmp_eq_u32 %[rn2], 0", f"s_cbranch_scc1 {lbl}"] + lines + [f"{lbl}:"]
+    """Skip an accumulator refill when the tile after next is an FP16 tile
+    (split: for this wave's half)."""
+    test = "s_bitcmp0_b32 %[rn2], %[half]" if LAYOUT["split"] else "s_cmp_eq_u32 %[rn2], 0"
+    return [test, f"s_cbranch_scc1 {lbl}"] + lines + [f"{lbl}:"]
+
+
+def to_int8_body(lbl: str) -> list[str]:
+    """Branch to lbl when the next tile to compute is an INT8 tile (split: for
+    this wave's half)."""
+    if LAYOUT["split"]:
+        return ["s_bitcmp1_b32 %[rn], %[half]", f"s_cbranch_scc1 {lbl}"]
+    return ["s_cmp_eq_u32 %[rn], 0", f"s_cbranch_scc0 {lbl}"]
 
 
 def b_chunks(kind: str, mixed_regs: bool, lbl: str) -> tuple[list[list[str]], list[str]]:
@@ -517,6 +552,13 @@ def copy_k(mode: str, par: int, lbl: str) -> list[str]:
     out: list[str] = []
     if mode == "mixed":
         out += ["s_bitcmp1_b64 %[bits], %[grp]", "s_cselect_b32 %[r2], 1, 0"]
+    elif mode == "split":
+        # bit 1: the high half's route; bit 0: the low half's, or the high
+        # half's for a tile past the low half's last key (%[t] = the tile)
+        out += ["s_bitcmp1_b64 %[bitsh], %[grp]", "s_cselect_b32 %[r2], 3, 0",
+                "s_cmp_ge_u32 %[t], %[lolim]", f"s_cbranch_scc1 {lbl}_past",
+                "s_and_b32 %[r2], %[r2], 2", "s_bitcmp1_b64 %[bits], %[grp]", "s_cselect_b32 %[t], 1, 0",
+                "s_or_b32 %[r2], %[r2], %[t]", f"{lbl}_past:"]
     elif mode == "i8":
         out += ["s_mov_b32 %[r2], 1"]
     else:
@@ -530,7 +572,7 @@ def copy_k(mode: str, par: int, lbl: str) -> list[str]:
         for i in range(K16_INS):
             if i:
                 o.append("v_add_u32 v%d, %%[stpk16], v%d" % (VO, VO))
-            o += [f"s_add_u32 m0, %[ldsw], {par * STAGE + i * NW * 1024}", "s_nop 0",
+            o += [f"s_add_u32 m0, %[ldsw], {par * LAYOUT['stage'] + i * NW * 1024}", "s_nop 0",
                   f"buffer_load_dwordx4 v{VO}, %[rsk16], 0 offen lds"]
         return o
 
@@ -539,8 +581,8 @@ def copy_k(mode: str, par: int, lbl: str) -> list[str]:
         for i in range(K8_INS):
             if i:
                 o.append("v_add_u32 v%d, %%[stpk8], v%d" % (VO, VO))
-            o += [f"s_add_u32 m0, %[ldsw], {par * STAGE + i * NW * 1024}", "s_nop 0",
-                  f"buffer_load_dwordx4 v{VO}, %[rsk8], 0 offen lds"]
+            o += [f"s_add_u32 m0, %[ldsw], {par * LAYOUT['stage'] + LAYOUT['k8off'] + i * NW * 1024}",
+                  "s_nop 0", f"buffer_load_dwordx4 v{VO}, %[rsk8], 0 offen lds"]
         # the tile's K scale (clamped lookup: the pointer stops at the last block)
         o += ["s_cmp_eq_u32 %[hask], 0", f"s_cbranch_scc1 {lbl}_nosk",
               f"buffer_load_ushort %[sk{par}], off, %[rssk], %[skoff]", f"s_branch {lbl}_skd",
@@ -551,6 +593,10 @@ def copy_k(mode: str, par: int, lbl: str) -> list[str]:
         out += k16()
     elif mode == "i8":
         out += k8()
+    elif mode == "split":
+        # fp16 K unless both halves are INT8, int8 K (and the scale) unless both are FP16
+        out += ["s_cmp_eq_u32 %[r2], 3", f"s_cbranch_scc1 {lbl}_n16"] + k16() + [f"{lbl}_n16:"]
+        out += ["s_cmp_eq_u32 %[r2], 0", f"s_cbranch_scc1 {lbl}_n8"] + k8() + [f"{lbl}_n8:"]
     else:
         out += ["s_cmp_eq_u32 %[r2], 0", f"s_cbranch_scc0 {lbl}_k8"]
         out += k16()
@@ -575,7 +621,7 @@ def copy_v(par: int) -> list[str]:
     for i in range(V16_INS):
         if i:
             o.append("v_add_u32 v%d, %%[stpv16], v%d" % (VO, VO))
-        o += [f"s_add_u32 m0, %[ldsw], {(1 - par) * STAGE + VOFF + i * NW * 1024}", "s_nop 0",
+        o += [f"s_add_u32 m0, %[ldsw], {(1 - par) * LAYOUT['stage'] + VOFF + i * NW * 1024}", "s_nop 0",
               f"buffer_load_dwordx4 v{VO}, %[rsv16], 0 offen lds"]
     return o + ["s_add_u32 %[tov16], %[tov16], %[tsv16]"]
 
@@ -625,16 +671,16 @@ def iteration(mode: str, par: int, lbl: str) -> list[str]:
     # a body with a next tile always copies V(n+1) (n + 1 < n_sw <= n_blocks)
     vsp = OPTS["v_spread"] and inner
     vg = copy_v_groups(par) if vsp else None
-    if mode in ("f16", "mixed"):
+    if mode != "i8":
         f16_body = body_iter("f16", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_f", cp("f", not vsp), vg)
-    if mode in ("i8", "mixed"):
+    if mode != "f16":
         i8_body = body_iter("i8", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_i", cp("i", not vsp), vg)
     if mode == "f16":
         out += f16_body
     elif mode == "i8":
         out += i8_body
     else:
-        out += ["s_cmp_eq_u32 %[rn], 0", f"s_cbranch_scc0 {lbl}_i8"]
+        out += to_int8_body(f"{lbl}_i8")
         out += f16_body
         out += [f"s_branch {lbl}_end", f"{lbl}_i8:"]
         out += i8_body
@@ -654,6 +700,8 @@ def fill(mode: str, lbl: str) -> list[str]:
     mixed_regs = mode != "f16"
     out = ["s_waitcnt vmcnt(0)", "s_barrier", "s_mov_b32 %[rn2], %[rn]"]
     out += ["s_cmp_le_u32 %[nblk], 1", f"s_cbranch_scc1 {lbl}_nok"]
+    if mode == "split":
+        out.append("s_mov_b32 %[t], 1")  # the copied tile, for its route
     out += copy_k(mode, 1, f"{lbl}_ck")
     out += ["s_mov_b32 %[rn2], %[r2]", f"{lbl}_nok:"]
     out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {lbl}_end"]
@@ -664,7 +712,7 @@ def fill(mode: str, lbl: str) -> list[str]:
     elif mode == "i8":
         out += i8_body
     else:
-        out += ["s_cmp_eq_u32 %[rn], 0", f"s_cbranch_scc0 {lbl}_i8"]
+        out += to_int8_body(f"{lbl}_i8")
         out += f16_body
         out += [f"s_branch {lbl}_end", f"{lbl}_i8:"]
         out += i8_body
@@ -673,6 +721,11 @@ def fill(mode: str, lbl: str) -> list[str]:
 
 
 def loop_asm(mode: str) -> list[str]:
+    with layout(mode):
+        return _loop_asm(mode)
+
+
+def _loop_asm(mode: str) -> list[str]:
     L = ".Lpipe%="
     # M0 carries the LDS address of every copy; the compiler's value of M0
     # is restored at the end (M0 is a reserved register).
@@ -715,8 +768,10 @@ def function(mode: str) -> str:
                 '[dk8] "v"(c.dk8)', '[sq16] "v"(c.sq16)', '[qks] "s"(c.qks)', '[magic2] "s"(c.magic2)']
         ins += [f'[k8a{i}] "v"(o.k8a[{i}])' for i in range(4)]
         ins += [f'[q8f{i}] "v"(o.q8f[{i}])' for i in range(4)]
-    if mode == "mixed":
+    if mode in ("mixed", "split"):
         ins += ['[bits] "s"(c.bits)']
+    if mode == "split":
+        ins += ['[bitsh] "s"(c.bits_hi)', '[lolim] "s"(c.lolim)', '[half] "s"(c.half)']
     text = "\n".join(f'      "{ln}\\n"' for ln in lines)
     clob = ", ".join(f'"v{r}"' for r in range(QA, VO + 1))
     return f'''__device__ __forceinline__ void pipe_loop_{mode}(PipeState& st, const PipeOps& o, PipeCopy& c) {{
@@ -759,7 +814,8 @@ struct PipeOps {
   i32x4 q8f[4];   // int8 Q codes (B operands of the int8 QK MFMAs)
   int ka[8];      // LDS byte addresses of the fp16 K operand reads, k-step 0..7 (stage 0)
   int k8a[4];     // the same for int8 K, k-step 0..3
-  int va[4];      // LDS byte addresses of the V^T reads, d block 0..3 (stage 0)
+  int va[4];      // LDS byte addresses of the V^T reads, d block 0..3 (stage 0's V slot;
+                  // the 16-bit read offsets then reach stage 1 of a split stage too)
   float fmax;     // FLT_MAX
 };
 
@@ -772,7 +828,10 @@ struct PipeCopy {
   int rn;                  // route of the next tile to compute
   uint32_t sk[2];          // K scale (fp16 bits) of the tiles of each parity
   int nsw, nblk, act;      // pipelined tiles, tiles, wave has rows
-  uint64_t bits;           // route bits of the workgroup's block
+  uint64_t bits;           // route bits of the workgroup's block (split: of its low half)
+  uint64_t bits_hi;        // split: route bits of the high half
+  int lolim;               // split: tiles from this one on lie past the low half's last key
+  int half;                // split: this wave's half (0 low, 1 high)
   int mt, kbt, hask;       // tiles per route group / per scale block, K scales present
   int sklast;              // byte offset of the sequence's last K scale of the head
   i32x4 rssk;              // buffer descriptor over the K scales
@@ -792,7 +851,7 @@ struct PipeCopy {
 
 def generate() -> str:
     parts = [HEADER]
-    for mode in ("f16", "i8", "mixed"):
+    for mode in ("f16", "i8", "mixed", "split"):
         parts.append(function(mode))
     parts.append("}  // namespace tmx\n")
     return "\n".join(parts)
