@@ -194,7 +194,7 @@ def test_lds_offsets_fit_and_stay_in_the_stages(mode):
 
 def _salu_route(lines, regs):
     """Runs the SALU route computation of a K copy (the lines up to the route
-    group advance) and returns %[r2]."""
+    group advance) and returns %[rn2]."""
     scc, i = 0, 0
     labels = {ln[:-1]: j for j, ln in enumerate(lines) if ln.endswith(":")}
     val = lambda a: regs[a[2:-1]] if a.startswith("%[") else int(a)
@@ -223,7 +223,7 @@ def _salu_route(lines, regs):
             regs[args[0][2:-1]] = val(args[1])
         else:
             raise AssertionError(f"unexpected instruction in the route block: {ln}")
-    return regs["r2"]
+    return regs["rn2"]
 
 
 def test_split_route_matches_the_kernels_tile_route():
@@ -256,21 +256,29 @@ def test_split_route_matches_the_kernels_tile_route():
     assert mismatches(lines, lambda lk: 0 if lk < 0 else lk // 64) > 0
 
 
+def _guard_tests(loop, tag):
+    """The test instruction of every refill guard (the line before its first
+    branch; a second guard reuses the first one's SCC)."""
+    return [loop[i - 1] for i, ln in enumerate(loop) if ln.startswith("s_cbranch_scc1") and ln.endswith(tag)]
+
+
 def test_split_loop_formats_and_wave_bits():
     """split: fp16 K is copied unless both halves are INT8 and int8 K unless
     both are FP16; each compute branch and refill guard tests this wave's bit
     of the two-bit route, never the whole route."""
-    loop = G.loop_asm("split")
-    text = "\n".join(loop)
-    assert "s_cmp_eq_u32 %[rn], 0" not in text and "s_cmp_eq_u32 %[rn2], 0" not in text
+    loop, mixed = G.loop_asm("split"), G.loop_asm("mixed")
+    assert "s_cmp_eq_u32 %[rn], 0" not in "\n".join(loop)
     assert sum(ln == "s_bitcmp1_b32 %[rn], %[half]" for ln in loop) == \
-        sum(ln == "s_cmp_eq_u32 %[rn], 0" for ln in G.loop_asm("mixed"))
-    assert sum(ln == "s_bitcmp0_b32 %[rn2], %[half]" for ln in loop) == \
-        sum(ln == "s_cmp_eq_u32 %[rn2], 0" for ln in G.loop_asm("mixed"))
+        sum(ln == "s_cmp_eq_u32 %[rn], 0" for ln in mixed) > 0
+    assert set(_guard_tests(loop, "_rfa")) == {"s_bitcmp0_b32 %[rn2], %[half]"}
+    assert set(_guard_tests(mixed, "_rfa")) == {"s_cmp_eq_u32 %[rn2], 0"}
+    assert len(_guard_tests(loop, "_rfa")) == len(_guard_tests(mixed, "_rfa")) > 0
+    # int8 routing: every tile after next is an INT8 tile, the refill is unconditional
+    assert not _guard_tests(G.loop_asm("i8"), "_rfa")
     with G.layout("split"):
         ck = G.copy_k("split", 1, ".Lt")
-    i16 = ck.index("s_cmp_eq_u32 %[r2], 3")
-    i8 = ck.index("s_cmp_eq_u32 %[r2], 0")
+    i16 = ck.index("s_cmp_eq_u32 %[rn2], 3")
+    i8 = ck.index("s_cmp_eq_u32 %[rn2], 0")
     assert i16 < i8
     assert all("rsk16" not in ln for ln in ck[i8:]) and any("rsk8" in ln for ln in ck[i8:])
     assert any("buffer_load_ushort" in ln for ln in ck[i8:])
@@ -292,7 +300,7 @@ def _planted(lines, pred, repl):
 def test_checker_catches_planted_violations(plant):
     body = BODIES["iter_f16_p0_True"]
     if plant == "drop_lds_wait":
-        bad = _planted(body, lambda ln: ln.startswith("s_waitcnt lgkmcnt(3)"), lambda ln: [])
+        bad = _planted(body, lambda ln: ln.startswith("s_waitcnt lgkmcnt("), lambda ln: [])
     elif plant == "early_conversion":
         # read the first QK accumulator pair right after the last QK MFMA
         idx = max(i for i, ln in enumerate(body) if ln.startswith("v_mfma_f32_32x32x16_f16 v[96:111]"))
@@ -307,8 +315,11 @@ def test_checker_catches_planted_violations(plant):
     elif plant == "permlane_no_nop":
         bad = _planted(body, lambda ln: ln == "s_nop 1", lambda ln: [])
     else:
+        # the copy's address add moved before its M0 write: the copy follows M0 at once
         loop = G.loop_asm("mixed")
-        bad = _planted(loop, lambda ln: ln == "s_nop 0", lambda ln: [])
+        i = next(i for i, ln in enumerate(loop) if ln.startswith("s_add_u32 m0"))
+        assert loop[i + 1].startswith("v_add_u32") and loop[i + 2].startswith("buffer_load")
+        bad = loop[:i] + [loop[i + 1], loop[i]] + loop[i + 2:]
         with pytest.raises(AssertionError):
             check_m0(bad)
         return
@@ -316,7 +327,7 @@ def test_checker_catches_planted_violations(plant):
         check_body(bad)
 
 
-_LEGACY = {"early": False, "v_ahead": False, "tail_first": False, "skip_refill": False}
+_LEGACY = {"early": False, "v_ahead": False, "tail_first": False, "skip_refill": False, "wait_pairs": False}
 OPTION_SETS = [{}, _LEGACY, {**_LEGACY, "copy_at": 1}, {**_LEGACY, "skip_rescale": True},
                {**_LEGACY, "qk_il": True}, {**_LEGACY, "pv_il": True}, {**_LEGACY, "early": True},
                {**_LEGACY, "v_ahead": True}, {**_LEGACY, "tail_first": True}, {"skip_rescale": True},
@@ -392,3 +403,16 @@ def test_bodies_read_operands_in_kstep_order():
     assert [int(ln.split("v")[-1]) - G.P for ln in dots] == list(range(16))
     i8 = [ln for ln in BODIES["iter_i8_p0_True"] if ln.startswith("v_mfma_i32_32x32x32_i8")]
     assert [int(re.search(r"%\[q8f(\d)\]", ln).group(1)) for ln in i8] == list(range(4)) * 2
+
+
+@pytest.mark.parametrize("mode", ["mixed", "split"])
+def test_fill_computes_tile0_with_its_own_route(mode):
+    """%[rn] holds tile 0's route until FILL has chosen tile 0's body: the K(1)
+    copy before FILL leaves tile 1's route in %[rn2], and %[rn] takes it only
+    after FILL (else tile 0 would be computed with tile 1's route)."""
+    loop = G.loop_asm(mode)
+    test = "s_cmp_eq_u32 %[rn], 0" if mode == "mixed" else "s_bitcmp1_b32 %[rn], %[half]"
+    first_test = loop.index(test)
+    first_write = next(i for i, ln in enumerate(loop) if ln.startswith("s_mov_b32 %[rn],"))
+    assert first_test < first_write
+    assert any(ln.startswith("s_cselect_b32 %[rn2]") for ln in loop[:first_test])

@@ -121,20 +121,23 @@ K16_INS, K8_INS, V16_INS = 4, 2, 4  # 1 KB copies per wave and tile
 #   auto_wait     LDS waits are recomputed from the operand registers (always
 #                 on with early / v_ahead);
 #   v_spread      in a body with a next tile, the four V copies go out one by
-#                 one after QK MFMAs 1, 3, 5 and 7 instead of with the K copy.
+#                 one after QK MFMAs 1, 3, 5 and 7 instead of with the K copy;
+#   wait_pairs    one LDS wait per two MFMAs (see auto_wait).
 OPTS = {"copy_at": None, "skip_refill": True, "skip_rescale": False, "qk_il": False, "pv_il": False,
-        "early": True, "v_ahead": True, "tail_first": True, "auto_wait": False, "v_spread": False}
+        "early": True, "v_ahead": True, "tail_first": True, "auto_wait": False, "v_spread": False,
+        "wait_pairs": True}
 
 # The launch the loop is generated for (loop_asm sets it per mode): the stage
 # size, the int8 K offset inside a stage, and whether routes are per half
 # (split: %[rn] / %[rn2] carry the low half's route in bit 0 and the high
 # half's in bit 1, and each wave tests bit %[half]).
-LAYOUT = {"stage": STAGE, "k8off": 0, "split": False}
+LAYOUT = {"stage": STAGE, "k8off": 0, "split": False, "mode": "mixed"}
 
 
 @contextmanager
 def layout(mode: str):
     saved = dict(LAYOUT)
+    LAYOUT["mode"] = mode
     if mode == "split":
         LAYOUT.update(stage=SPLIT_STAGE, k8off=SPLIT_K8OFF, split=True)
     try:
@@ -371,13 +374,25 @@ def _regs(tok: str) -> set[int]:
     return out
 
 
+def _next_mfma(lines: list[str], k: int) -> str | None:
+    """The next MFMA after line k in straight-line code (None past a label or
+    a branch)."""
+    for ln in lines[k + 1:]:
+        if ln.endswith(":") or ln.startswith("s_cbranch") or ln.startswith("s_branch"):
+            return None
+        if ln.startswith("v_mfma"):
+            return ln
+    return None
+
+
 def auto_wait(lines: list[str]) -> list[str]:
     """The body's LDS waits, recomputed as the minimal ones: before an
     instruction that reads or overwrites the destination of an outstanding
     LDS read, wait until that read has returned (LDS reads return in order).
-    The full drain a body starts with is kept.  The only branches inside a
-    body skip blocks without LDS reads, so both paths see the same
-    outstanding reads."""
+    OPTS['wait_pairs']: a wait before an MFMA also covers the outstanding
+    reads of the next MFMA, which then needs none (half the waits).  A full
+    drain at the body's start is kept.  The only branches inside a body skip
+    blocks without LDS reads, so both paths see the same outstanding reads."""
     out: list[str] = []
     pending: list[set[int]] = []
     for k, ln in enumerate(lines):
@@ -393,6 +408,10 @@ def auto_wait(lines: list[str]) -> list[str]:
         hit = [j for j, d in enumerate(pending) if d & regs]
         if hit:
             j = max(hit)
+            nxt = _next_mfma(lines, k) if OPTS["wait_pairs"] and op.startswith("v_mfma") else None
+            if nxt is not None:
+                regs2 = _regs(nxt.partition(" ")[2])
+                j = max([j] + [i for i, d in enumerate(pending) if d & regs2])
             out.append(f"s_waitcnt lgkmcnt({len(pending) - 1 - j})")
             pending = pending[j + 1:]
         out.append(ln)
@@ -432,11 +451,29 @@ def guard_rescale(lines: list[str], lbl: str) -> list[str]:
     return [f"s_cbranch_vccz {lbl}"] + lines + [f"{lbl}:"]
 
 
-def guard_refill(lines: list[str], lbl: str) -> list[str]:
+def guard_refill(lines: list[str], lbl: str, test: bool = True) -> list[str]:
     """Skip an accumulator refill when the tile after next is an FP16 tile
-    (split: for this wave's half)."""
-    test = "s_bitcmp0_b32 %[rn2], %[half]" if LAYOUT["split"] else "s_cmp_eq_u32 %[rn2], 0"
-    return [test, f"s_cbranch_scc1 {lbl}"] + lines + [f"{lbl}:"]
+    (split: for this wave's half).  test=False: SCC still holds the test of
+    the previous guard (body_iter checks that nothing in between writes SCC).
+    With int8 routing every tile is an INT8 tile: always refill."""
+    if LAYOUT["mode"] == "i8":
+        return list(lines)
+    t = ["s_bitcmp0_b32 %[rn2], %[half]" if LAYOUT["split"] else "s_cmp_eq_u32 %[rn2], 0"] if test else []
+    return t + [f"s_cbranch_scc1 {lbl}"] + lines + [f"{lbl}:"]
+
+
+_NO_SCC = ("s_nop", "s_waitcnt", "s_cbranch", "s_branch", "s_barrier", "s_setprio")
+
+
+def check_scc_kept(lines: list[str], lbl_a: str, lbl_b: str) -> None:
+    """No instruction between the end of guard lbl_a and the branch to lbl_b
+    writes SCC (so the second guard may reuse the first one's test)."""
+    if f"{lbl_a}:" not in lines or f"s_cbranch_scc1 {lbl_b}" not in lines:
+        return
+    i, j = lines.index(f"{lbl_a}:"), lines.index(f"s_cbranch_scc1 {lbl_b}")
+    for ln in lines[i + 1:j]:
+        if ln.startswith("s_") and not ln.startswith(_NO_SCC):
+            raise AssertionError(f"SCC written between the refill guards: {ln}")
 
 
 def to_int8_body(lbl: str) -> list[str]:
@@ -483,7 +520,7 @@ def b_chunks(kind: str, mixed_regs: bool, lbl: str) -> tuple[list[list[str]], li
             fa, fb = refill(QA), refill(QB)
             if OPTS["skip_refill"]:
                 ch[9] = ch[9] + guard_refill(fa, f"{lbl}_rfa")
-                ch[14] = ch[14] + guard_refill(fb, f"{lbl}_rfb")
+                ch[14] = ch[14] + guard_refill(fb, f"{lbl}_rfb", test=False)
             else:
                 ch[8] = ch[8] + fa[:4]
                 ch[9] = ch[9] + fa[4:]
@@ -500,7 +537,9 @@ def body_iter(kind: str, kslot: int, vslot: int, mixed_regs: bool, par_next: int
         pre.append("v_cmp_neq_f32 vcc, 1.0, %[al]")
     if kind == "i8":
         pre += int8_scale(par_next)
-    out = ["s_waitcnt lgkmcnt(0)"]
+    # no LDS read is outstanding when a body starts (the previous body's
+    # reads were all consumed by its MFMAs)
+    out: list[str] = []
     if not early:
         out, pre = out + pre, []
     elif kind == "none":
@@ -518,8 +557,9 @@ def body_iter(kind: str, kslot: int, vslot: int, mixed_regs: bool, par_next: int
         out += phase_a(kind, kslot, softmax_steps() + rescale(0), copy, None, pre, vs, vgroups)
     ch, tail = b_chunks(kind, mixed_regs, lbl)
     out += phase_b(vslot, ch, tail, pre_read=v_ahead or (early and kind == "none"))
-    if early or v_ahead or OPTS["auto_wait"]:
+    if early or v_ahead or OPTS["auto_wait"] or OPTS["wait_pairs"]:
         out = pad_valu_mfma(auto_wait(out))
+    check_scc_kept(out, f"{lbl}_rfa", f"{lbl}_rfb")
     return out
 
 
@@ -544,45 +584,57 @@ def body_fill(kind: str, kslot: int, mixed_regs: bool, lbl: str = ".Lf") -> list
 
 
 # ---- copies and bookkeeping (SALU / VMEM) ---------------------------------------
+#
+# A wave issues at most one instruction per issue slot, and on gfx950 every
+# s_waitcnt, s_nop and SALU instruction costs a wave about as much issue time
+# as a VALU instruction (probe: ~4 clk each, a taken branch 7-10 clk, also
+# with two waves per SIMD).  The bookkeeping below is therefore branch-free
+# where it can be, the M0 write of a copy is separated from the copy by the
+# copy's own address add instead of an s_nop, and the loop tests the drain
+# and the waves without rows once per item instead of once per tile.
+
+def routed(mode: str) -> bool:
+    """The route of a tile comes from the route bits (else it is constant)."""
+    return mode in ("mixed", "split")
+
+
+def _copy(dest: int, addr: str, rsrc: str) -> list[str]:
+    """One 1 KB copy: M0 (LDS destination), the lane's address (the one wait
+    state M0 needs before the copy), the LDS-DMA load."""
+    return [f"s_add_u32 m0, %[ldsw], {dest}", addr, f"buffer_load_dwordx4 v{VO}, %[{rsrc}], 0 offen lds"]
+
 
 def copy_k(mode: str, par: int, lbl: str) -> list[str]:
-    """K(t) for t = n + 2 into K slot par, with its route (-> %[r2]), its K
-    scale (-> scale register par) and the bookkeeping advance of the C++
-    issue_next_k: route group, scale block, tile offsets."""
+    """K(t) for t = n + 2 (in %[t]) into K slot par, with its route (->
+    %[rn2]), its K scale (-> scale register par) and the bookkeeping advance
+    of the C++ issue_next_k: route group, scale block, tile offsets."""
     out: list[str] = []
     if mode == "mixed":
-        out += ["s_bitcmp1_b64 %[bits], %[grp]", "s_cselect_b32 %[r2], 1, 0"]
+        out += ["s_bitcmp1_b64 %[bits], %[grp]", "s_cselect_b32 %[rn2], 1, 0"]
     elif mode == "split":
         # bit 1: the high half's route; bit 0: the low half's, or the high
-        # half's for a tile past the low half's last key (%[t] = the tile)
-        out += ["s_bitcmp1_b64 %[bitsh], %[grp]", "s_cselect_b32 %[r2], 3, 0",
+        # half's for a tile past the low half's last key
+        out += ["s_bitcmp1_b64 %[bitsh], %[grp]", "s_cselect_b32 %[rn2], 3, 0",
                 "s_cmp_ge_u32 %[t], %[lolim]", f"s_cbranch_scc1 {lbl}_past",
-                "s_and_b32 %[r2], %[r2], 2", "s_bitcmp1_b64 %[bits], %[grp]", "s_cselect_b32 %[t], 1, 0",
-                "s_or_b32 %[r2], %[r2], %[t]", f"{lbl}_past:"]
-    elif mode == "i8":
-        out += ["s_mov_b32 %[r2], 1"]
-    else:
-        out += ["s_mov_b32 %[r2], 0"]
-    # route group: ++gc == mask_tiles -> gc = 0, ++grp
-    out += ["s_add_u32 %[gc], %[gc], 1", "s_cmp_eq_u32 %[gc], %[mt]", "s_cselect_b32 %[gc], 0, %[gc]",
-            "s_addc_u32 %[grp], %[grp], 0"]
+                "s_and_b32 %[rn2], %[rn2], 2", "s_bitcmp1_b64 %[bits], %[grp]", "s_cselect_b32 %[t], 1, 0",
+                "s_or_b32 %[rn2], %[rn2], %[t]", f"{lbl}_past:"]
+    if routed(mode):
+        # route group: ++gc == mask_tiles -> gc = 0, ++grp
+        out += ["s_add_u32 %[gc], %[gc], 1", "s_cmp_eq_u32 %[gc], %[mt]", "s_cselect_b32 %[gc], 0, %[gc]",
+                "s_addc_u32 %[grp], %[grp], 0"]
 
     def k16() -> list[str]:
-        o = ["v_add_u32 v%d, %%[tok16], %%[dk16]" % VO]
+        o: list[str] = []
         for i in range(K16_INS):
-            if i:
-                o.append("v_add_u32 v%d, %%[stpk16], v%d" % (VO, VO))
-            o += [f"s_add_u32 m0, %[ldsw], {par * LAYOUT['stage'] + i * NW * 1024}", "s_nop 0",
-                  f"buffer_load_dwordx4 v{VO}, %[rsk16], 0 offen lds"]
+            addr = (f"v_add_u32 v{VO}, %[tok16], %[dk16]" if i == 0 else f"v_add_u32 v{VO}, %[stpk16], v{VO}")
+            o += _copy(par * LAYOUT["stage"] + i * NW * 1024, addr, "rsk16")
         return o
 
     def k8() -> list[str]:
-        o = ["v_add_u32 v%d, %%[tok8], %%[dk8]" % VO]
+        o: list[str] = []
         for i in range(K8_INS):
-            if i:
-                o.append("v_add_u32 v%d, %%[stpk8], v%d" % (VO, VO))
-            o += [f"s_add_u32 m0, %[ldsw], {par * LAYOUT['stage'] + LAYOUT['k8off'] + i * NW * 1024}",
-                  "s_nop 0", f"buffer_load_dwordx4 v{VO}, %[rsk8], 0 offen lds"]
+            addr = (f"v_add_u32 v{VO}, %[tok8], %[dk8]" if i == 0 else f"v_add_u32 v{VO}, %[stpk8], v{VO}")
+            o += _copy(par * LAYOUT["stage"] + LAYOUT["k8off"] + i * NW * 1024, addr, "rsk8")
         # the tile's K scale (clamped lookup: the pointer stops at the last block)
         o += ["s_cmp_eq_u32 %[hask], 0", f"s_cbranch_scc1 {lbl}_nosk",
               f"buffer_load_ushort %[sk{par}], off, %[rssk], %[skoff]", f"s_branch {lbl}_skd",
@@ -595,34 +647,33 @@ def copy_k(mode: str, par: int, lbl: str) -> list[str]:
         out += k8()
     elif mode == "split":
         # fp16 K unless both halves are INT8, int8 K (and the scale) unless both are FP16
-        out += ["s_cmp_eq_u32 %[r2], 3", f"s_cbranch_scc1 {lbl}_n16"] + k16() + [f"{lbl}_n16:"]
-        out += ["s_cmp_eq_u32 %[r2], 0", f"s_cbranch_scc1 {lbl}_n8"] + k8() + [f"{lbl}_n8:"]
+        out += ["s_cmp_eq_u32 %[rn2], 3", f"s_cbranch_scc1 {lbl}_n16"] + k16() + [f"{lbl}_n16:"]
+        out += ["s_cmp_eq_u32 %[rn2], 0", f"s_cbranch_scc1 {lbl}_n8"] + k8() + [f"{lbl}_n8:"]
     else:
-        out += ["s_cmp_eq_u32 %[r2], 0", f"s_cbranch_scc0 {lbl}_k8"]
+        out += ["s_cmp_eq_u32 %[rn2], 0", f"s_cbranch_scc0 {lbl}_k8"]
         out += k16()
         out += [f"s_branch {lbl}_kd", f"{lbl}_k8:"]
         out += k8()
         out += [f"{lbl}_kd:"]
-    out += ["s_add_u32 %[tok16], %[tok16], %[tsk16]"]
+    if mode != "i8":
+        out += ["s_add_u32 %[tok16], %[tok16], %[tsk16]"]
     if mode != "f16":
         out += ["s_add_u32 %[tok8], %[tok8], %[tsk8]",
-                # scale block: ++sc == kb_tiles -> sc = 0 and the pointer moves
-                # to the next block unless it is at the sequence's last one
-                "s_add_u32 %[sc], %[sc], 1", "s_cmp_eq_u32 %[sc], %[kbt]", f"s_cbranch_scc0 {lbl}_nsb",
-                "s_mov_b32 %[sc], 0", "s_cmp_eq_u32 %[skoff], %[sklast]", f"s_cbranch_scc1 {lbl}_nsb",
-                "s_add_u32 %[skoff], %[skoff], %[hk2]",
-                f"{lbl}_nsb:"]
+                # scale block: ++sc == kb_tiles -> sc = 0 and the offset moves to
+                # the next block, clamped at the sequence's last one (offsets of
+                # one head's blocks are hk2 apart, so the clamp stops exactly there)
+                "s_add_u32 %[sc], %[sc], 1", "s_cmp_eq_u32 %[sc], %[kbt]", "s_cselect_b32 %[sc], 0, %[sc]",
+                "s_cselect_b32 %[t], %[hk2], 0", "s_add_u32 %[skoff], %[skoff], %[t]",
+                "s_min_u32 %[skoff], %[skoff], %[sklast]"]
     return out
 
 
 def copy_v(par: int) -> list[str]:
     """V(t) for t = n + 1 into V slot 1 - par."""
-    o = ["v_add_u32 v%d, %%[tov16], %%[dv16]" % VO]
+    o: list[str] = []
     for i in range(V16_INS):
-        if i:
-            o.append("v_add_u32 v%d, %%[stpv16], v%d" % (VO, VO))
-        o += [f"s_add_u32 m0, %[ldsw], {(1 - par) * LAYOUT['stage'] + VOFF + i * NW * 1024}", "s_nop 0",
-              f"buffer_load_dwordx4 v{VO}, %[rsv16], 0 offen lds"]
+        addr = (f"v_add_u32 v{VO}, %[tov16], %[dv16]" if i == 0 else f"v_add_u32 v{VO}, %[stpv16], v{VO}")
+        o += _copy((1 - par) * LAYOUT["stage"] + VOFF + i * NW * 1024, addr, "rsv16")
     return o + ["s_add_u32 %[tov16], %[tov16], %[tsv16]"]
 
 
@@ -640,84 +691,97 @@ def copy_v_groups(par: int) -> list[list[str]]:
     return groups
 
 
-def copies(mode: str, par: int, lbl: str, with_v: bool = True) -> list[str]:
-    """Iteration n's copies: K(n+2) while n + 2 <= n_sw and n + 2 < n_blocks
-    (its route -> %[rn2]), V(n+1) while n + 1 < n_blocks."""
-    out = ["s_add_u32 %[t], %[n], 2", "s_cmp_gt_u32 %[t], %[nsw]", f"s_cbranch_scc1 {lbl}_nok",
-           "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nok"]
+def copies(mode: str, par: int, lbl: str, with_v: bool = True, v_always: bool = False) -> list[str]:
+    """Iteration n's copies: K(n+2) while n + 2 <= %[klim] = min(n_sw,
+    n_blocks - 1) (its route -> %[rn2]), V(n+1) while n + 1 < n_blocks
+    (v_always: a body with a next tile, where n + 1 < n_sw <= n_blocks)."""
+    out = ["s_add_u32 %[t], %[n], 2", "s_cmp_gt_u32 %[t], %[klim]", f"s_cbranch_scc1 {lbl}_nok"]
     out += copy_k(mode, par, f"{lbl}_ck")
-    out += ["s_mov_b32 %[rn2], %[r2]", f"{lbl}_nok:"]
+    out += [f"{lbl}_nok:"]
     if not with_v:
         return out
+    if v_always:
+        return out + copy_v(par)
     out += ["s_add_u32 %[t], %[n], 1", "s_cmp_ge_u32 %[t], %[nblk]", f"s_cbranch_scc1 {lbl}_nov"]
     out += copy_v(par)
     return out + [f"{lbl}_nov:"]
 
 
+def _tile_start(mode: str) -> list[str]:
+    """Every iteration: this wave's copies have landed, then every wave's; the
+    route of the tile after next starts as the next tile's (no K copy)."""
+    out = ["s_waitcnt vmcnt(0)", "s_barrier"]
+    return out + (["s_mov_b32 %[rn2], %[rn]"] if routed(mode) else [])
+
+
+def _tile_end(mode: str) -> list[str]:
+    return ["s_mov_b32 %[rn], %[rn2]"] if routed(mode) else []
+
+
 def iteration(mode: str, par: int, lbl: str) -> list[str]:
-    """Iteration n (n & 1 == par; %[n] holds n)."""
+    """Iteration n (n & 1 == par; %[n] holds n) of an active wave, n + 1 < n_sw:
+    a body with a next tile (FP16 or INT8 by the next tile's route)."""
     mixed_regs = mode != "f16"
     inner = OPTS["copy_at"] is not None or OPTS["early"]
-    out = ["s_waitcnt vmcnt(0)", "s_barrier", "s_mov_b32 %[rn2], %[rn]"]
-    if not inner:
-        out += copies(mode, par, f"{lbl}_c")
-    # compute (waves whose rows all lie past the sequence end only copy)
-    out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {lbl}_inact",
-            "s_add_u32 %[t], %[n], 1", "s_cmp_ge_u32 %[t], %[nsw]", f"s_cbranch_scc1 {lbl}_drain"]
-
-    def cp(tag: str, with_v: bool = True) -> list[str] | None:
-        return copies(mode, par, f"{lbl}_{tag}c", with_v) if inner else None
-
-    # a body with a next tile always copies V(n+1) (n + 1 < n_sw <= n_blocks)
+    out = _tile_start(mode)
     vsp = OPTS["v_spread"] and inner
     vg = copy_v_groups(par) if vsp else None
-    if mode != "i8":
-        f16_body = body_iter("f16", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_f", cp("f", not vsp), vg)
-    if mode != "f16":
-        i8_body = body_iter("i8", 1 - par, par, mixed_regs, 1 - par, f"{lbl}_i", cp("i", not vsp), vg)
+    cps = copies(mode, par, f"{lbl}_c", not vsp, v_always=True)
+    if not inner:
+        out += cps
+
+    def body(kind: str, tag: str) -> list[str]:
+        cp = copies(mode, par, f"{lbl}_{tag}c", not vsp, v_always=True) if inner else None
+        return body_iter(kind, 1 - par, par, mixed_regs, 1 - par, f"{lbl}_{tag}", cp, vg)
+
     if mode == "f16":
-        out += f16_body
+        out += body("f16", "f")
     elif mode == "i8":
-        out += i8_body
+        out += body("i8", "i")
     else:
         out += to_int8_body(f"{lbl}_i8")
-        out += f16_body
+        out += body("f16", "f")
         out += [f"s_branch {lbl}_end", f"{lbl}_i8:"]
-        out += i8_body
-    out += [f"s_branch {lbl}_end", f"{lbl}_drain:"]
-    out += body_iter("none", 0, par, mixed_regs, 0, f"{lbl}_d", cp("d"))
-    out += [f"s_branch {lbl}_end", f"{lbl}_inact:"]
-    if inner:
-        out += copies(mode, par, f"{lbl}_xc")
-    out += [f"{lbl}_end:", "s_mov_b32 %[rn], %[rn2]"]
-    return out
+        out += body("i8", "i")
+        out += [f"{lbl}_end:"]
+    return out + _tile_end(mode)
+
+
+def drain(mode: str, par: int, lbl: str) -> list[str]:
+    """The last iteration (n = n_sw - 1) of an active wave: no next tile."""
+    out = _tile_start(mode)
+    out += body_iter("none", 0, par, mode != "f16", 0, f"{lbl}_d", copies(mode, par, f"{lbl}_dc"))
+    return out + _tile_end(mode)
+
+
+def inactive(mode: str, par: int, lbl: str) -> list[str]:
+    """Iteration n of a wave whose rows all lie past the sequence end: only the
+    barrier and the copies."""
+    return _tile_start(mode) + copies(mode, par, f"{lbl}_xc") + _tile_end(mode)
+
+
+def fill_copy(mode: str, lbl: str) -> list[str]:
+    """The barrier after the prologue (the Q block's use of stage 1 ends, K(0)
+    and V(0) have landed) and the copy of K(1): iteration -1 (parity 1) of
+    the copy schedule, for every wave.  %[rn] stays tile 0's route (FILL
+    computes tile 0) until the caller moves tile 1's into it."""
+    out = _tile_start(mode)
+    out += ["s_cmp_le_u32 %[nblk], 1", f"s_cbranch_scc1 {lbl}_nok", "s_mov_b32 %[t], 1"]
+    out += copy_k(mode, 1, f"{lbl}_ck")
+    return out + [f"{lbl}_nok:"]
 
 
 def fill(mode: str, lbl: str) -> list[str]:
-    """The barrier after the prologue (the Q block's use of stage 1 ends, K(0)
-    and V(0) have landed), the copy of K(1), tile 0's QK, conversion and
-    maximum.  Runs as iteration -1 (parity 1) of the copy schedule."""
+    """Tile 0's QK, conversion and maximum (active waves)."""
     mixed_regs = mode != "f16"
-    out = ["s_waitcnt vmcnt(0)", "s_barrier", "s_mov_b32 %[rn2], %[rn]"]
-    out += ["s_cmp_le_u32 %[nblk], 1", f"s_cbranch_scc1 {lbl}_nok"]
-    if mode == "split":
-        out.append("s_mov_b32 %[t], 1")  # the copied tile, for its route
-    out += copy_k(mode, 1, f"{lbl}_ck")
-    out += ["s_mov_b32 %[rn2], %[r2]", f"{lbl}_nok:"]
-    out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {lbl}_end"]
-    f16_body = body_fill("f16", 0, mixed_regs, f"{lbl}_bf")
-    i8_body = body_fill("i8", 0, mixed_regs, f"{lbl}_bi")
+    f16_body = body_fill("f16", 0, mixed_regs, f"{lbl}_bf") if mode != "i8" else []
+    i8_body = body_fill("i8", 0, mixed_regs, f"{lbl}_bi") if mode != "f16" else []
     if mode == "f16":
-        out += f16_body
-    elif mode == "i8":
-        out += i8_body
-    else:
-        out += to_int8_body(f"{lbl}_i8")
-        out += f16_body
-        out += [f"s_branch {lbl}_end", f"{lbl}_i8:"]
-        out += i8_body
-    out += [f"{lbl}_end:", "s_mov_b32 %[rn], %[rn2]"]
-    return out
+        return f16_body
+    if mode == "i8":
+        return i8_body
+    return to_int8_body(f"{lbl}_i8") + f16_body + [f"s_branch {lbl}_end", f"{lbl}_i8:"] + i8_body + \
+        [f"{lbl}_end:"]
 
 
 def loop_asm(mode: str) -> list[str]:
@@ -729,13 +793,26 @@ def _loop_asm(mode: str) -> list[str]:
     L = ".Lpipe%="
     # M0 carries the LDS address of every copy; the compiler's value of M0
     # is restored at the end (M0 is a reserved register).
-    out = ["s_mov_b32 %[m0s], m0"]
-    out += fill(mode, f"{L}_f")
-    out += ["s_mov_b32 %[n], 0", f"{L}_loop:"]
+    out = ["s_mov_b32 %[m0s], m0",
+           "s_sub_u32 %[klim], %[nblk], 1", "s_min_u32 %[klim], %[klim], %[nsw]",
+           "s_sub_u32 %[nsw1], %[nsw], 1", "s_mov_b32 %[n], 0"]
+    out += fill_copy(mode, f"{L}_fc")
+    out += ["s_cmp_eq_u32 %[act], 0", f"s_cbranch_scc1 {L}_xin"]
+    out += fill(mode, f"{L}_f") + _tile_end(mode)
+    # iterations 0 .. n_sw - 2 have a next tile; n_sw - 1 is the drain
+    out += ["s_cmp_eq_u32 %[nsw1], 0", f"s_cbranch_scc1 {L}_d0", f"{L}_loop:"]
     out += iteration(mode, 0, f"{L}_p0")
-    out += ["s_add_u32 %[n], %[n], 1", "s_cmp_ge_u32 %[n], %[nsw]", f"s_cbranch_scc1 {L}_done"]
+    out += ["s_add_u32 %[n], %[n], 1", "s_cmp_ge_u32 %[n], %[nsw1]", f"s_cbranch_scc1 {L}_d1"]
     out += iteration(mode, 1, f"{L}_p1")
-    out += ["s_add_u32 %[n], %[n], 1", "s_cmp_lt_u32 %[n], %[nsw]", f"s_cbranch_scc1 {L}_loop"]
+    out += ["s_add_u32 %[n], %[n], 1", "s_cmp_lt_u32 %[n], %[nsw1]", f"s_cbranch_scc1 {L}_loop", f"{L}_d0:"]
+    out += drain(mode, 0, f"{L}_q0")
+    out += [f"s_branch {L}_done", f"{L}_d1:"]
+    out += drain(mode, 1, f"{L}_q1")
+    out += [f"s_branch {L}_done", f"{L}_xin:"] + _tile_end(mode) + [f"{L}_inact:"]
+    out += inactive(mode, 0, f"{L}_x0")
+    out += ["s_add_u32 %[n], %[n], 1", "s_cmp_ge_u32 %[n], %[nsw]", f"s_cbranch_scc1 {L}_done"]
+    out += inactive(mode, 1, f"{L}_x1")
+    out += ["s_add_u32 %[n], %[n], 1", "s_cmp_lt_u32 %[n], %[nsw]", f"s_cbranch_scc1 {L}_inact"]
     out += [f"{L}_done:",
             # the C++ code after the statement reads the O accumulators: the
             # last PV MFMAs' results are read 36 wait states after them
@@ -749,8 +826,8 @@ def function(mode: str) -> str:
             '"+{v[48:63]}"(st.acc[3])', '"+{v[64:79]}"(st.s16)',
             '[mn] "+v"(st.mn)', '[al] "+v"(st.al)', '[ng] "+v"(st.ng)', '[li] "+v"(st.li)',
             '[tok16] "+s"(c.tok16)', '[tov16] "+s"(c.tov16)', '[grp] "+s"(c.grp)', '[gc] "+s"(c.gc)',
-            '[rn] "+s"(c.rn)', '[n] "=&s"(n)', '[t] "=&s"(t)', '[r2] "=&s"(r2)', '[rn2] "=&s"(rn2)',
-            '[m0s] "=&s"(m0s)']
+            '[rn] "+s"(c.rn)', '[n] "=&s"(n)', '[t] "=&s"(t)', '[rn2] "=&s"(rn2)',
+            '[m0s] "=&s"(m0s)', '[klim] "=&s"(klim)', '[nsw1] "=&s"(nsw1)']
     ins = ['[nsw] "s"(c.nsw)', '[nblk] "s"(c.nblk)', '[act] "s"(c.act)', '[mt] "s"(c.mt)',
            '[ldsw] "s"(c.ldsw)', '[rsk16] "s"(c.rsk16)', '[rsv16] "s"(c.rsv16)',
            '[stpk16] "s"(c.stpk16)', '[stpv16] "s"(c.stpv16)', '[tsk16] "s"(c.tsk16)', '[tsv16] "s"(c.tsv16)',
@@ -775,7 +852,7 @@ def function(mode: str) -> str:
     text = "\n".join(f'      "{ln}\\n"' for ln in lines)
     clob = ", ".join(f'"v{r}"' for r in range(QA, VO + 1))
     return f'''__device__ __forceinline__ void pipe_loop_{mode}(PipeState& st, const PipeOps& o, PipeCopy& c) {{
-  int n, t, r2, rn2, m0s;
+  int n, t, rn2, m0s, klim, nsw1;
   asm volatile(
 {text}
       : {", ".join(outs)}
