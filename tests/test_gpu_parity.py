@@ -24,6 +24,11 @@ QUANT_CASES = [
     ("ragged", [1, 63, 64, 65, 300], 3, 128),
     ("with_empty", [1000, 0, 129], 2, 64),
     ("d256_five_heads", [300, 20], 5, 256),  # blk 128 x d 256: the streamed (two-pass) path
+    # the K pre-pass shapes of the attention entry (8 / 2 / 1 KV heads, head_dim
+    # 128) with ragged, one-token and empty sequences
+    ("rows_k_shape", [300, 1, 63, 64, 65, 0, 129], 8, 128),
+    ("rows_two_heads", [333, 17], 2, 128),
+    ("rows_one_head", [200, 5, 64], 1, 128),
 ]
 
 
