@@ -416,3 +416,45 @@ def test_fill_computes_tile0_with_its_own_route(mode):
     first_write = next(i for i, ln in enumerate(loop) if ln.startswith("s_mov_b32 %[rn],"))
     assert first_test < first_write
     assert any(ln.startswith("s_cselect_b32 %[rn2]") for ln in loop[:first_test])
+
+
+def _walk(lines, take):
+    """Instruction classes executed along one path through straight-line code
+    with forward branches (take(label) decides each conditional branch)."""
+    labels = {ln[:-1]: i for i, ln in enumerate(lines) if ln.endswith(":")}
+    counts = {}
+    i = 0
+    while i < len(lines):
+        ln = lines[i]
+        i += 1
+        if ln.endswith(":"):
+            continue
+        op = ln.split()[0]
+        if op.startswith("s_cbranch") or op == "s_branch":
+            counts["branch"] = counts.get("branch", 0) + 1
+            tgt = ln.split()[1]
+            if op == "s_branch" or take(tgt):
+                i = labels[tgt]
+            continue
+        k = ("mfma" if op.startswith("v_mfma") else "lds" if op.startswith("ds_") else
+             "vmem" if op.startswith("buffer_") else "wait" if op == "s_waitcnt" else
+             "nop" if op == "s_nop" else "salu" if op.startswith("s_") else "valu")
+        counts[k] = counts.get(k, 0) + 1
+    return counts
+
+
+def test_iteration_instruction_budget():
+    """The mixed loop's iteration on an FP16 tile (K of an FP16 tile copied,
+    refill skipped) keeps its lean shape: one LDS wait per two MFMAs, no
+    s_nop per copy, the drain / row-less checks outside the iteration.  Every
+    such instruction costs a wave an issue slot."""
+    with G.layout("mixed"):
+        lines = G.iteration("mixed", 0, ".L0")
+
+    def take(t):
+        return t.endswith("_rfa") or t.endswith("_rfb") or t.endswith("_end")
+
+    c = _walk(lines, take)
+    assert c["mfma"] == 32 and c["lds"] == 48 and c["vmem"] == 8
+    assert c["wait"] <= 18 and c.get("nop", 0) <= 2
+    assert c["salu"] + c["branch"] <= 38, c
