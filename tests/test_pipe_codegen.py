@@ -12,6 +12,9 @@
     - an MFMA reads a VALU result no sooner than 3 wait states after it;
     - no instruction reads the result of the v_exp_f32 right before it;
     - v_permlane32_swap's operands were written at least 2 wait states earlier;
+    - the result of a DOT instruction (v_dot2c) is read or overwritten by any
+      other instruction no sooner than 3 wait states after it (the next
+      v_dot2c accumulating into it excepted);
     - a copy (buffer_load ... lds) is at least one wait state after the M0
       write it uses.
   Each rule is shown to catch a planted violation.
@@ -71,6 +74,7 @@ def check_body(lines: list[str]) -> None:
     valu_w: dict[int, int] = {}     # reg -> clock of the last VALU write
     clock = 0
     prev_exp: set[int] = set()
+    dot_w: dict[int, int] = {}      # reg -> clock of the last v_dot2c write
     for line in lines:
         if line.endswith(":") or not line:
             continue
@@ -98,6 +102,9 @@ def check_body(lines: list[str]) -> None:
             srcs |= dst
         assert not (srcs & inflight), f"reads an LDS destination before its wait: {line}"
         assert not (srcs & prev_exp), f"reads the exp result of the previous instruction: {line}"
+        if op != "v_dot2c_f32_f16":
+            for r in (srcs | dst) & set(dot_w):
+                assert clock - dot_w[r] >= 4, f"uses a DOT result within 3 wait states: {line}"
         if op.startswith("v_mfma"):
             c_regs = _regs(args[3]) if len(args) > 3 else set()
             for r in srcs:
@@ -122,6 +129,11 @@ def check_body(lines: list[str]) -> None:
                 valu_w[r] = clock
                 mfma_w.pop(r, None)
         prev_exp = dst if op == "v_exp_f32" else set()
+        for r in dst:
+            if op == "v_dot2c_f32_f16":
+                dot_w[r] = clock
+            else:
+                dot_w.pop(r, None)
         clock += ws
 
 
@@ -296,7 +308,7 @@ def _planted(lines, pred, repl):
 
 
 @pytest.mark.parametrize("plant", ["drop_lds_wait", "early_conversion", "rescale_late", "exp_then_use",
-                                   "permlane_no_nop", "m0_no_nop"])
+                                   "permlane_no_nop", "m0_no_nop", "dot_then_use"])
 def test_checker_catches_planted_violations(plant):
     body = BODIES["iter_f16_p0_True"]
     if plant == "drop_lds_wait":
@@ -312,6 +324,10 @@ def test_checker_catches_planted_violations(plant):
         idx = next(i for i, ln in enumerate(body) if ln.startswith("v_exp_f32 v"))
         r = _parse(body[idx])[1][0]
         bad = body[:idx + 1] + [f"v_mov_b32 v{G.T + 5}, {r}"] + body[idx + 1:]
+    elif plant == "dot_then_use":
+        # the l update right behind the last row-sum step
+        idx = max(i for i, ln in enumerate(body) if ln.startswith("v_dot2c_f32_f16"))
+        bad = body[:idx + 1] + [f"v_add_f32 %[li], %[li], v{G.LS}"] + body[idx + 1:]
     elif plant == "permlane_no_nop":
         bad = _planted(body, lambda ln: ln == "s_nop 1", lambda ln: [])
     else:

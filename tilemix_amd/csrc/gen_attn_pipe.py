@@ -70,7 +70,10 @@ VALU write to an O block or to the INT8 accumulators precedes the MFMA that
 reads it by at least three wait states (pad_valu_mfma inserts the s_nop where
 the schedule does not provide them); an exp result is never read by the next
 instruction; v_permlane32_swap's operand is written two wait states earlier;
-one wait state separates an M0 write from the LDS-DMA copy that uses it.  LDS
+the row sum a v_dot2c chain accumulates (a DOT result) is read or overwritten
+by another instruction no sooner than three wait states after the last
+v_dot2c (the l update reads it a whole phase later); one wait state
+separates an M0 write from the LDS-DMA copy that uses it.  LDS
 waits count only the statement's own reads (every compute body starts with
 s_waitcnt lgkmcnt(0), and the scale loads are VMEM loads); auto_wait derives
 them from the operand registers of each read's first use.
