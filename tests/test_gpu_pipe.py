@@ -182,3 +182,26 @@ def test_pipe_random_split_launches_bitwise(device, seed):
     print(f"pipe vs C++ body {case}: {same.mean():.6f} identical", flush=True)
     assert np.isfinite(got).all()
     assert same.all(), (name, np.argwhere(~same)[:5])
+
+
+@pytest.mark.parametrize("case", [c for c in CASES if c[0] in ("short_and_ragged", "split_short_and_ragged",
+                                                               "long_causal_int8")],
+                         ids=lambda c: c[0])
+def test_group_interleave_keeps_outputs(device, case):
+    """The work order (TILEMIX_HIP_INTERLEAVE: 1-4 groups of an XCD interleaved
+    item by item) changes no output bit: every work item is computed once and
+    on its own."""
+    inputs = _inputs(case, 23)
+    outs = []
+    old = os.environ.get("TILEMIX_HIP_INTERLEAVE")
+    try:
+        for ilv in ("1", "2", "3", "4"):
+            os.environ["TILEMIX_HIP_INTERLEAVE"] = ilv
+            outs.append(_launch(device, inputs, case, pipe=True))
+    finally:
+        if old is None:
+            os.environ.pop("TILEMIX_HIP_INTERLEAVE", None)
+        else:
+            os.environ["TILEMIX_HIP_INTERLEAVE"] = old
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint16), outs[0].view(np.uint16))

@@ -213,6 +213,13 @@ int launch_attn(const tilemix_attn_params& p, int32_t* dump_i32, void* dump_f16,
     a.pipe = (env != nullptr && env[0] == '0') ? 0 : 1;
   }
   a.per_xcd = (int)work_items_per_xcd((int64_t)p.heads_k * p.batch, (int64_t)m_blocks * a.group);
+  // Groups interleaved per XCD (the work order only: outputs do not depend on
+  // it); TILEMIX_HIP_INTERLEAVE=1..4 overrides the choice.
+  a.ilv = interleave_groups(p.max_seqlen_k, p.head_dim);
+  {
+    const char* env = getenv("TILEMIX_HIP_INTERLEAVE");
+    if (env != nullptr && env[0] >= '1' && env[0] <= '4' && env[1] == '\0') a.ilv = env[0] - '0';
+  }
 
   const int dp = p.head_dim <= 64 ? 64 : 128;
   dispatch_attn(a, kind, dp, p.routing_mode, int8v, dump, p.bias != nullptr, gen, stream);

@@ -46,29 +46,55 @@ struct AttnKArgs {
   int total_items;  // (sequence, query head, query block) work items
   int per_xcd;
   int pipe;         // the pipelined assembly tile body may serve this launch
+  int ilv;          // groups of an XCD interleaved item by item (interleave_groups)
 };
 
 // Work item of workgroup `bid`, or -1.  Items are numbered
 // ((z * hk + kv_head) * m_blocks + mrev) * group + g, so one (sequence, kv head)
-// "group" is ipg = m_blocks * group consecutive items.  Workgroups reach the 8
-// XCDs round-robin (bid & 7); the j-th workgroup of XCD x takes
-//   * while whole rounds of 8 groups remain: group x + 8 (j / ipg), item
-//     j % ipg -- a group stays on one XCD (its L2 serves every re-read of the
-//     group's K/V tiles) and groups are dealt round-robin, so every XCD gets
-//     the same mix of long and short sequences;
+// "group" is ipg = m_blocks * group consecutive items, its query blocks
+// longest first.  Workgroups reach the 8 XCDs round-robin (bid & 7); the j-th
+// workgroup of XCD x takes
+//   * while whole rounds of 8 groups remain: from XCD x's groups x, x + 8,
+//     x + 16, ... -- a group stays on one XCD (its L2 serves every re-read of
+//     the group's K/V tiles) and groups are dealt round-robin, so every XCD
+//     gets the same mix of long and short sequences.  The XCD's groups run ilv
+//     at a time, interleaved item by item (chunk c = j / (ilv ipg) holds groups
+//     c ilv .. c ilv + kc - 1, kc = min(ilv, groups left); position w = j mod
+//     (ilv ipg) takes item w / kc of group c ilv + w mod kc): the last items
+//     dispatched are then the short query blocks of ilv groups instead of
+//     every block of the last group, which shortens the launch's tail, as
+//     long as ilv groups' K/V stay in the XCD's L2 (interleave_groups);
 //   * for the last G % 8 groups: their items dealt over all 8 XCDs (item
 //     8 j' + x), which also covers a launch with fewer than 8 groups.
 // per_xcd (the grid is 8 * per_xcd) = (G / 8) * ipg + ceil((G % 8) * ipg / 8).
 __host__ __device__ inline int64_t work_items_per_xcd(int64_t groups, int64_t ipg) {
   return (groups / 8) * ipg + ((groups % 8) * ipg + 7) / 8;
 }
-__host__ __device__ __forceinline__ int work_item(int bid, int total_items, int ipg) {
+__host__ __device__ __forceinline__ int work_item(int bid, int total_items, int ipg, int ilv) {
   const int x = bid & 7, j = bid >> 3;
   const int groups = total_items / ipg;
-  const int full_j = (groups / 8) * ipg;  // workgroups per XCD in whole rounds
-  if (j < full_j) return (x + 8 * (j / ipg)) * ipg + j % ipg;
-  const int item = (groups / 8) * 8 * ipg + 8 * (j - full_j) + x;
+  const int gpx = groups / 8;            // whole-round groups per XCD
+  const int full_j = gpx * ipg;          // workgroups per XCD in whole rounds
+  if (j < full_j) {
+    const int c = j / (ilv * ipg);
+    const int kc = min(ilv, gpx - c * ilv);
+    const int w = j - c * ilv * ipg;
+    return (x + 8 * (c * ilv + w % kc)) * ipg + w / kc;
+  }
+  const int item = gpx * 8 * ipg + 8 * (j - full_j) + x;
   return item < total_items ? item : -1;
+}
+
+// Groups interleaved per XCD (work_item): as many as keep their K/V tiles
+// (fp16 K and V, int8 K: 5 bytes per key and head-dim column) within ~5.5 MB,
+// a little over one XCD's 4 MB L2, at most 4.  Measured on cfg2-like
+// launches: 4096 keys (2.6 MB per group) -> 2, 2048 keys -> 4 (-2.6% / -4.3%
+// kernel time); 8192-key groups stay at 1 (2 or 4 of them thrash the L2:
+// +15% / +46%).
+__host__ __device__ inline int interleave_groups(int64_t max_seqlen_k, int head_dim) {
+  const int64_t group_bytes = max_seqlen_k * (int64_t)head_dim * 5;
+  const int64_t k = group_bytes > 0 ? (int64_t)(5632 * 1024) / group_bytes : 4;
+  return k < 1 ? 1 : k > 4 ? 4 : (int)k;
 }
 
 typedef __attribute__((address_space(3))) void lds_void;

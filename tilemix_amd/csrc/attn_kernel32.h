@@ -106,7 +106,7 @@ attn32_kernel(const AttnKArgs a) {
 
   // ---- work item ---------------------------------------------------------
   const int bid = blockIdx.x;
-  const int lam = work_item(bid, a.total_items, a.m_blocks * a.group);
+  const int lam = work_item(bid, a.total_items, a.m_blocks * a.group, a.ilv);
   if (lam < 0) return;
   int t = lam;
   const int g = t % a.group;
