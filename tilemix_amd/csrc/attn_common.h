@@ -216,7 +216,13 @@ __device__ __forceinline__ float2 pair32(float x) {
 // compiler cannot tell the stage being filled from the stage being read and
 // waits for the copy before every LDS read, which serialises the prefetch with
 // the tile's compute.  rsrc and lds are wave-uniform (SGPRs); M0 carries the
-// LDS address, and one wait state separates its write from the load.
+// LDS address.  Five wait states precede the load: one is what an M0 write
+// needs before it, five what a VALU write of an SGPR (v_readfirstlane, or a
+// v_readlane that reloads a spilled descriptor) needs before a VMEM
+// instruction reads that SGPR -- the compiler pads its own loads for both,
+// but not a load inside an asm statement, and without the padding a spilled
+// buffer descriptor reloaded right before the copy was read half-updated
+// (a memory fault).  tests/test_asm_hazards.py scans every instantiation.
 struct SRsrc {
   i32x4 w;
 };
@@ -241,7 +247,7 @@ __device__ __forceinline__ uint32_t lds_addr(const unsigned char* p) {
 }
 __device__ __forceinline__ void async_load16_asm(const SRsrc& rs, int voffset, uint32_t lds) {
   asm volatile(
-      "s_nop 0\n\t"
+      "s_nop 4\n\t"
       "buffer_load_dwordx4 %0, %1, 0 offen lds"
       :
       : "v"(voffset), "s"(rs.w), "{m0}"(lds)
