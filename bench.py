@@ -123,6 +123,19 @@ def time_steps(fn, steps: int, warmup: int):
     return start.elapsed_time(end) / steps  # ms per step
 
 
+def interleaved(fns, rounds: int, per: int, timer):
+    """Samples of each function, timed round-robin: each of `rounds` rounds
+    times every function in turn, `per` calls each, through
+    `timer(fn, per) -> list of samples`.  Clock drift over the run and the
+    caches a function leaves warm for its own next call then favour none of
+    them."""
+    out = [[] for _ in fns]
+    for _ in range(rounds):
+        for i, f in enumerate(fns):
+            out[i].extend(timer(f, per))
+    return out
+
+
 def time_each(fn, steps: int):
     """Per-launch HIP-event durations (events on the launch stream)."""
     import torch
@@ -461,16 +474,11 @@ def main() -> int:
     # favour whichever is timed first; likewise the steps -------------------
     _, bm0 = sptrans_map(0.0, device)
     per = max(1, -(-args.steps // TIMING_ROUNDS))
-    kfns = (kernel_fn(bm50), kernel_fn(bm0), kernel_fn(bm0, "fp16"))
-    kt = [[] for _ in kfns]
-    st50, st0 = [], []
-    for _ in range(TIMING_ROUNDS):
-        for i, f in enumerate(kfns):
-            kt[i].extend(time_each(f, per))
-        st50.append(time_steps(step_fn(bm50), per, 2))
-        st0.append(time_steps(step_fn(bm0), per, 2))
+    step_timer = lambda f, n: [time_steps(f, n, 2)]  # one sample (ms per step) per round
+    kt = interleaved((kernel_fn(bm50), kernel_fn(bm0), kernel_fn(bm0, "fp16")), TIMING_ROUNDS, per, time_each)
+    st = interleaved((step_fn(bm50), step_fn(bm0)), TIMING_ROUNDS, per, step_timer)
     k_ms50_rounds, k_ms_fp16map, k_ms_fp16mode = (statistics.mean(t) for t in kt)
-    ms50_rounds, ms_fp16map = statistics.median(st50), statistics.median(st0)
+    ms50_rounds, ms_fp16map = (statistics.median(t) for t in st)
     t_roof = roofline_seconds(f50, ops)
     achieved = ops / (k_ms * 1e-3) / 1e12
     peak = ops / t_roof / 1e12
@@ -478,18 +486,14 @@ def main() -> int:
     sweep = None
     if not args.no_sweep:
         ps = (0.0, 0.25, 0.5, 0.75, 1.0)
-        maps = {p: sptrans_map(p, device) for p in ps}
-        kp = {p: [] for p in ps}
-        sp = {p: [] for p in ps}
-        for _ in range(TIMING_ROUNDS):
-            for p in ps:
-                kp[p].extend(time_each(kernel_fn(maps[p][1]), per))
-                sp[p].append(time_steps(step_fn(maps[p][1]), per, 2))
+        maps = [sptrans_map(p, device) for p in ps]
+        kp = interleaved([kernel_fn(m[1]) for m in maps], TIMING_ROUNDS, per, time_each)
+        sp = interleaved([step_fn(m[1]) for m in maps], TIMING_ROUNDS, per, step_timer)
         sweep = {}
-        for p in ps:
-            fp = int8_fraction(maps[p][0].tolist())
-            kms = statistics.mean(kp[p])
-            sweep[str(p)] = {"int8_fraction": fp, "step_ms": statistics.median(sp[p]), "kernel_ms": kms,
+        for i, p in enumerate(ps):
+            fp = int8_fraction(maps[i][0].tolist())
+            kms = statistics.mean(kp[i])
+            sweep[str(p)] = {"int8_fraction": fp, "step_ms": statistics.median(sp[i]), "kernel_ms": kms,
                              "kernel_roofline_frac": roofline_seconds(fp, ops) / (kms * 1e-3)}
 
     others = None

@@ -38,3 +38,17 @@ def test_more_than_one_gpu_is_refused():
                        timeout=120, cwd=REPO)
     assert r.returncode == 2
     assert "one MI355X" in r.stderr
+
+
+def test_interleaved_timing_alternates():
+    # Every function gets rounds x per samples, and the calls alternate
+    # function by function in every round (no function timed all at once).
+    calls = []
+
+    def timer(f, n):
+        calls.append((f, n))
+        return [f] * n
+
+    out = bench.interleaved(("a", "b", "c"), 5, 4, timer)
+    assert calls == [(f, 4) for _ in range(5) for f in ("a", "b", "c")]
+    assert out == [["a"] * 20, ["b"] * 20, ["c"] * 20]
