@@ -197,6 +197,33 @@ def e2e_prefill(device, runs: int = 20, warmup: int = 5, seed: int = 0):
     return statistics.median(times), times
 
 
+def glue_kernel_fn(device, block_m: int = 64):
+    """The attention launch of the model glue's shape alone (the kernel that
+    other_configs times as glue_L2048_block_m64): cfg2 heads at B8 x 2048,
+    SpTrans50 (stride 128, c 32), K quantised once, Q inside the kernel."""
+    import torch
+    from tilemix_amd.attention import precision_maps as pm
+    from tilemix_amd.attention.hip import tilemix as tmx
+    from tilemix_amd.attention.hip.tilemix import _quantize_for_launch
+    lg, bg = 2048, 8
+    g = torch.Generator(device=device)
+    g.manual_seed(6)
+    q = torch.randn((bg * lg, HQ, D), generator=g, device=device).half()
+    k = torch.randn((bg * lg, HK, D), generator=g, device=device).half()
+    v = torch.randn((bg * lg, HK, D), generator=g, device=device).half()
+    cu = torch.arange(0, (bg + 1) * lg, lg, dtype=torch.int32, device=device)
+    row = pm.make_precision_bitmask(lg, block_m, 64, None, percentage=0.5, pattern_type="sptrans",
+                                    pattern_params={"stride": 128, "c": 32}, COMPUTE_BLOCK_N=64)
+    bm = row.repeat(HK).to(device)
+    k8, sk, cuk = _quantize_for_launch(k, cu, lg, 64)
+    v8, sv, cuv = tmx._dummy_v_quantization_metadata(v, cu)
+    return lambda: tmx.launch_prequantized(
+        q, k, v, cu, cu, lg, lg, bm, q8=None, k8=k8, v8=v8, sQ_blocks=None, sK_blocks=sk, sV_blocks=sv,
+        cu_q_scale=None, cu_k_scale=cuk, cu_v_scale=cuv, block_m=block_m, block_n=64, block_n_mask=64,
+        BLKQ=128, BLKK=64, causal=True, scalar_scales=(block_m == 128), int8_use_fp16_v=True,
+        routing_mode="mixed", _q_in_kernel=True)
+
+
 def other_configs(device, steps: int):
     """BASELINE configs 3 and 4 (parity-test shapes, reported for information):
     one tilemix_attention_with_quant step each, effective TOPS and the blended
@@ -385,6 +412,9 @@ def main() -> int:
                     help="skip the SpTrans p-sweep, configs 1/3/4 and the glue shapes")
     ap.add_argument("--kernel-only", type=int, default=0, metavar="N",
                     help="profiling mode: launch only the SpTrans50 attention kernel N times, print nothing else")
+    ap.add_argument("--glue-kernel-only", type=int, default=0, metavar="N",
+                    help="profiling mode: launch only the model glue's attention kernel (B8 x 2048, cfg2 heads, "
+                         "SpTrans50, block_m 64) N times, print nothing else")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="MIB",
                     help="profiling mode: one device copy of MIB MiB (HBM counter calibration)")
     ap.add_argument("--e2e-only", type=int, default=0, metavar="N",
@@ -409,6 +439,18 @@ def main() -> int:
         dst.copy_(src)
         torch.cuda.synchronize()
         print(f"copied {args.copy_calibration} MiB", flush=True)
+        return 0
+    if args.glue_kernel_only:
+        fn = glue_kernel_fn(device)
+        fn()
+        a = torch.randn(8192, 8192, device=device, dtype=torch.float16)
+        for _ in range(600):
+            a @ a
+        torch.cuda.synchronize()
+        for _ in range(args.glue_kernel_only):
+            fn()
+        torch.cuda.synchronize()
+        print(f"launched the glue attention kernel {args.glue_kernel_only + 1} times", flush=True)
         return 0
     if args.e2e_only:
         med, times = e2e_prefill(device, runs=args.e2e_only, warmup=1)
